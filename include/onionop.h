@@ -1,0 +1,230 @@
+/*
+ * onionop.h -- C ABI of libonionop_hip.so, the gfx950 (MI355X) implementation of
+ * NNop's fused-kernel hot path: flash attention (causal, pair bias, GQA, key padding),
+ * online softmax, RMS norm, layer norm and Llama RoPE, forward and backward.
+ *
+ * Every entry point replaces the body of one host launcher of the reference package
+ * (MurrellGroup/ONIONop.jl, Julia module NNop); the reference file:line is given at
+ * each declaration.  The public Julia functions and their ChainRules rrules stay as
+ * they are and call these through `ccall`.
+ *
+ * Conventions
+ *  - Arrays are dense and column-major, exactly as the Julia arrays they replace:
+ *    an array documented as (d1, d2, d3, d4) has d1 contiguous.  (The same memory is
+ *    a row-major C/torch tensor of shape (d4, d3, d2, d1).)
+ *  - Dimensions are int64_t.  Element types are given by the ONIONOP_F32/F16/BF16
+ *    codes below; statistics that travel from a forward to its backward (ms, ls,
+ *    rstd, mu) are always float32.
+ *  - `stream` is a hipStream_t (NULL = the default stream).  Every call only
+ *    enqueues work on it; nothing synchronises, nothing allocates device memory.
+ *    Workspace, where needed, is passed in by the caller; its size comes from the
+ *    matching *_workspace() query.
+ *  - Every call returns ONIONOP_OK (0) or a negative ONIONOP_E_* status.  The text
+ *    of the last error of the calling thread is returned by onionop_last_error().
+ *    Shape errors carry the reference's own messages.
+ *  - All pointers are device pointers, except where stated.
+ */
+#ifndef ONIONOP_H
+#define ONIONOP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum onionop_dtype { ONIONOP_F32 = 0, ONIONOP_F16 = 1, ONIONOP_BF16 = 2 };
+
+enum onionop_status {
+    ONIONOP_OK = 0,
+    ONIONOP_E_SHAPE = -1,        /* shape / size mismatch (reference `error(...)`, `@assert`) */
+    ONIONOP_E_DTYPE = -2,        /* unknown or unsupported element type                       */
+    ONIONOP_E_UNSUPPORTED = -3,  /* valid request this build has no kernel for (e.g. E=256)   */
+    ONIONOP_E_HIP = -4,          /* a HIP runtime call failed                                  */
+    ONIONOP_E_NULL = -5,         /* a required pointer is NULL                                 */
+    ONIONOP_E_WORKSPACE = -6     /* workspace missing or smaller than the *_workspace() size   */
+};
+
+/* Message of the last failed call on this thread ("" if none).  Host pointer, owned
+ * by the library, valid until the next call on the same thread. */
+const char* onionop_last_error(void);
+
+/* ABI revision of this header (bumped on any signature change). */
+int onionop_abi_version(void);
+#define ONIONOP_ABI_VERSION 1
+
+/* LDS bytes per workgroup of `device` (cached once per device).
+ * Replaces NNop.shared_memory / _shared_memory(::ROCBackend)
+ * (src/NNop.jl:27-30, ext/NNopAMDGPUExt.jl:6-9). */
+int onionop_device_lds_bytes(int device, size_t* bytes_out /* host pointer */);
+
+/* ------------------------------------------------------------------ attention */
+
+/*
+ * Flash attention forward.  Replaces the body of `_flash_attention`
+ * (src/attention.jl:145-197) and its kernel `_flash_attention_fwd!`
+ * (src/attention.jl:8-143).
+ *   q    (E, QL, QH, B)        dtype
+ *   k, v (E, KL, KH, B)        dtype
+ *   pair (QH, QL, KL, B)       dtype, nullable: additive bias after scaling
+ *   kpad (KL, B)               uint8 (Julia Bool), nullable: 0 = masked key
+ *   o    (E, QL, QH, B)        dtype, output, normalised
+ *   ms, ls (QL, QH, B)         float32 outputs: running row max and row denominator of
+ *                              the online softmax, carried to the backward
+ * scale multiplies Q.K before the bias; the reference passes T(1/sqrt(E))
+ * (src/attention.jl:166).  E must be a power of two in {16, 32, 64, 128};
+ * QH % KH == 0 (q head j uses kv head j / (QH/KH), src/attention.jl:36).
+ * Rows whose keys are all masked give o = 0, ms = -Inf, ls = 0 (the reference
+ * produces NaN there).
+ */
+int onionop_flash_attn_fwd(void* stream, int dtype,
+                           int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B,
+                           const void* q, const void* k, const void* v,
+                           const void* pair, const uint8_t* kpad,
+                           int causal, float scale,
+                           void* o, float* ms, float* ls);
+
+/* Bytes of workspace onionop_flash_attn_bwd needs for these sizes. */
+size_t onionop_flash_attn_bwd_workspace(int dtype, int64_t E, int64_t QL, int64_t KL,
+                                        int64_t QH, int64_t KH, int64_t B);
+
+/*
+ * Flash attention backward.  Replaces the body of `∇flash_attention`
+ * (src/attention_bwd.jl:213-303) with its kernels `_flash_attention_bwd_preprocess!`
+ * (src/attention_bwd.jl:177-211) and `_flash_attention_bwd!` (src/attention_bwd.jl:1-175).
+ *   dO   (E, QL, QH, B)        dtype, cotangent of o (dense)
+ *   o, ms, ls                  as produced by onionop_flash_attn_fwd
+ *   q, k, v, pair, kpad, causal, scale  as given to the forward
+ *   dq   (E, QL, QH, B), dk, dv (E, KL, KH, B)   dtype outputs (overwritten)
+ *   dpair (QH, QL, KL, B)      dtype output, required iff pair != NULL (overwritten;
+ *                              entries of causally masked pairs are 0)
+ * qk_fp16 != 0 rounds Q and K to float16 before every product that uses them, as the
+ * reference backward does for every element type (src/attention_bwd.jl:20-21,
+ * src/attention.jl:219); it only changes results for dtype F32.  GQA gradients are
+ * summed over the q heads of a group without atomics (deterministic).
+ */
+int onionop_flash_attn_bwd(void* stream, int dtype,
+                           int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B,
+                           const void* dO, const void* o, const float* ms, const float* ls,
+                           const void* q, const void* k, const void* v,
+                           const void* pair, const uint8_t* kpad,
+                           int causal, float scale, int qk_fp16,
+                           void* dq, void* dk, void* dv, void* dpair,
+                           void* workspace, size_t workspace_bytes);
+
+/*
+ * The three stages onionop_flash_attn_bwd runs, callable one by one (same arguments,
+ * same workspace; call them in this order on one stream).
+ *  _preprocess: delta = rowsum(dO .* o) and the log-sum-exp of every query row into the
+ *               workspace.  Replaces `_flash_attention_bwd_preprocess!`
+ *               (src/attention_bwd.jl:177-211).
+ *  _dkdv:       dk, dv.  With _dq, replaces `_flash_attention_bwd!`
+ *               (src/attention_bwd.jl:1-175).
+ *  _dq:         dq and dpair.
+ */
+int onionop_flash_attn_bwd_preprocess(void* stream, int dtype, int64_t E, int64_t QL, int64_t QH, int64_t B,
+                                      const void* dO, const void* o, const float* ms, const float* ls,
+                                      void* workspace, size_t workspace_bytes);
+int onionop_flash_attn_bwd_dkdv(void* stream, int dtype,
+                                int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B,
+                                const void* dO, const void* q, const void* k, const void* v,
+                                const void* pair, const uint8_t* kpad, int causal, float scale, int qk_fp16,
+                                void* dk, void* dv, void* workspace, size_t workspace_bytes);
+int onionop_flash_attn_bwd_dq(void* stream, int dtype,
+                              int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B,
+                              const void* dO, const void* q, const void* k, const void* v,
+                              const void* pair, const uint8_t* kpad, int causal, float scale, int qk_fp16,
+                              void* dq, void* dpair, void* workspace, size_t workspace_bytes);
+
+/* -------------------------------------------------------------------- softmax */
+
+/*
+ * Online softmax over dim 1 of x (N, M): y[:, j] = exp(x[:, j] - max) / sum.
+ * Replaces `online_softmax` (src/softmax.jl:60-68) and its kernel
+ * `online_softmax!` (src/softmax.jl:19-58).  Computed in float32; y has x's dtype.
+ */
+int onionop_softmax_fwd(void* stream, int dtype, int64_t N, int64_t M,
+                        const void* x, void* y);
+
+/*
+ * Softmax backward: dx = y .* dy - y .* sum(y .* dy; dims=1).
+ * Replaces `∇online_softmax` (src/softmax.jl:70-80), which the reference runs as
+ * broadcasts plus a reduction.  dy, y, dx share `dtype`.
+ */
+int onionop_softmax_bwd(void* stream, int dtype, int64_t N, int64_t M,
+                        const void* dy, const void* y, void* dx);
+
+/* ------------------------------------------------------------------- RMS norm */
+
+/*
+ * y = (offset + w) .* x .* rstd, rstd = 1/sqrt(mean(x.^2; dims=1) + eps).
+ * Replaces `_rms_norm` (src/rms_norm.jl:117-137) and `_rms_norm!` (src/rms_norm.jl:3-38).
+ *   x (emb, n) dtype_x, w (emb) dtype_w, y (emb, n) dtype_x, rstd (n) float32.
+ */
+int onionop_rms_norm_fwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n,
+                         const void* x, const void* w, float eps, float offset,
+                         void* y, float* rstd);
+
+size_t onionop_rms_norm_bwd_workspace(int64_t emb, int64_t n);
+
+/*
+ * RMS norm backward.  Replaces `∇rms_norm` (src/rms_norm.jl:139-169) and
+ * `_∇rms_norm!` (src/rms_norm.jl:43-115), including the column sum of the dw
+ * partials (src/rms_norm.jl:162-167), which runs here as a second fused kernel.
+ *   dy (emb, n) dtype_x, rstd (n) f32, x, w as forward.
+ *   dx (emb, n) dtype_x, dw (emb) float32 (the reference returns Float32 dw).
+ */
+int onionop_rms_norm_bwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n,
+                         const void* dy, const float* rstd, const void* x, const void* w,
+                         float offset, void* dx, float* dw,
+                         void* workspace, size_t workspace_bytes);
+
+/* ----------------------------------------------------------------- layer norm */
+
+/*
+ * y = (x - mu) .* rstd .* w .+ b with biased variance, two-pass.
+ * Replaces `_layer_norm` (src/layer_norm.jl:150-170) and `_layer_norm!`
+ * (src/layer_norm.jl:8-63).
+ *   x (emb, n) dtype_x; w, b (emb) dtype_w; y (emb, n) dtype_x; mu, rstd (n) float32.
+ */
+int onionop_layer_norm_fwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n,
+                           const void* x, const void* w, const void* b, float eps,
+                           void* y, float* mu, float* rstd);
+
+size_t onionop_layer_norm_bwd_workspace(int64_t emb, int64_t n);
+
+/*
+ * Layer norm backward.  Replaces `∇layer_norm` (src/layer_norm.jl:172-204) and
+ * `_∇layer_norm!` (src/layer_norm.jl:65-148), including the partial sums
+ * (src/layer_norm.jl:197-202), accumulated here in float32 and rounded once.
+ *   dx (emb, n) dtype_x; dw, db (emb) dtype_w.
+ */
+int onionop_layer_norm_bwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n,
+                           const void* dy, const float* mu, const float* rstd,
+                           const void* x, const void* w,
+                           void* dx, void* dw, void* db,
+                           void* workspace, size_t workspace_bytes);
+
+/* ----------------------------------------------------------------------- RoPE */
+
+/*
+ * Llama (rotate-half, non-interleaved) rotary embedding of q and k, out of place.
+ * Replaces `_llama_rope` (src/rope/llama_rope.jl:69-89) and `llama_rope!`
+ * (src/rope/llama_rope.jl:24-65); `llama_rope` is sin_sign = +1, `∇llama_rope`
+ * is sin_sign = -1 (src/rope/llama_rope.jl:86,91-92).
+ *   q (E, L, QH, B), k (E, L, KH, B) dtype; cos, sin (E, L, B) float32, of which
+ *   rows 1..E/2 are read; q_out, k_out like q, k (may alias q, k).
+ * For i < E/2, j = i + E/2:  out_i = x_i c - x_j s,  out_j = x_j c + x_i s,
+ * with c = cos[i], s = sin_sign * sin[i].
+ */
+int onionop_llama_rope(void* stream, int dtype, int64_t E, int64_t L,
+                       int64_t QH, int64_t KH, int64_t B,
+                       const void* q, const void* k, const float* cos, const float* sin,
+                       float sin_sign, void* q_out, void* k_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ONIONOP_H */

@@ -1,0 +1,339 @@
+// abi.hip -- the extern "C" entry points of libonionop_hip.so declared in
+// include/onionop.h: argument validation (with the reference's error messages),
+// workspace sizing, and dispatch to the kernel launchers.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/onionop.h"
+#include "launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_err[0] = 0;
+    return ONIONOP_OK;
+}
+
+// Status of the launches just enqueued on this thread.
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(ONIONOP_E_HIP, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool valid_dt(int dt) { return dt == ONIONOP_F32 || dt == ONIONOP_F16 || dt == ONIONOP_BF16; }
+size_t dt_size(int dt) { return dt == ONIONOP_F32 ? 4 : 2; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+const char* dt_name(int dt) { return dt == 0 ? "Float32" : dt == 1 ? "Float16" : dt == 2 ? "BFloat16" : "?"; }
+
+// Shape checks of _flash_attention / ∇flash_attention (src/attention.jl:153-156,
+// src/attention_bwd.jl:224-227) plus what this build supports.
+int check_attn(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B) {
+    if (!valid_dt(dtype)) return fail(ONIONOP_E_DTYPE, "flash_attention: unsupported element type code %d", dtype);
+    if (E < 0 || QL < 0 || KL < 0 || QH < 0 || KH < 0 || B < 0)
+        return fail(ONIONOP_E_SHAPE, "flash_attention: negative dimension");
+    if (!is_pow2(E)) return fail(ONIONOP_E_SHAPE, "Only power-of-2 embedding dims are supported.");
+    if (KH == 0 || QH % KH != 0)
+        return fail(ONIONOP_E_SHAPE, "Number of query heads `%lld` must be divisible by number of KV heads `%lld`.",
+                    (long long)QH, (long long)KH);
+    if (E < 16 || E > 128)
+        return fail(ONIONOP_E_UNSUPPORTED, "flash_attention: embedding dim %lld not supported (16, 32, 64 or 128)",
+                    (long long)E);
+    if (QL > (1LL << 30) || KL > (1LL << 30) || QH > 65535 || B > 65535)
+        return fail(ONIONOP_E_UNSUPPORTED, "flash_attention: dimensions too large");
+    return ok();
+}
+
+std::mutex g_lds_mu;
+size_t g_lds[64];
+bool g_lds_set[64];
+
+}  // namespace
+
+extern "C" {
+
+const char* onionop_last_error(void) { return g_err; }
+
+int onionop_abi_version(void) { return ONIONOP_ABI_VERSION; }
+
+int onionop_device_lds_bytes(int device, size_t* bytes_out) {
+    if (bytes_out == nullptr) return fail(ONIONOP_E_NULL, "onionop_device_lds_bytes: bytes_out is NULL");
+    if (device < 0 || device >= 64) return fail(ONIONOP_E_SHAPE, "onionop_device_lds_bytes: bad device %d", device);
+    std::lock_guard<std::mutex> lock(g_lds_mu);
+    if (!g_lds_set[device]) {
+        hipDeviceProp_t prop;
+        const hipError_t e = hipGetDeviceProperties(&prop, device);
+        if (e != hipSuccess) return fail(ONIONOP_E_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+        g_lds[device] = prop.sharedMemPerBlock;
+        g_lds_set[device] = true;
+    }
+    *bytes_out = g_lds[device];
+    return ok();
+}
+
+// ------------------------------------------------------------------ attention
+
+int onionop_flash_attn_fwd(void* stream, int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
+                           int64_t B, const void* q, const void* k, const void* v, const void* pair,
+                           const uint8_t* kpad, int causal, float scale, void* o, float* ms, float* ls) {
+    int st = check_attn(dtype, E, QL, KL, QH, KH, B);
+    if (st) return st;
+    const bool any_q = QL * QH * B > 0, any_k = KL * KH * B > 0;
+    if ((any_q && (!q || !o || !ms || !ls)) || (any_q && any_k && (!k || !v)))
+        return fail(ONIONOP_E_NULL, "flash_attention: NULL tensor pointer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+        return fail(ONIONOP_E_SHAPE, "flash_attention: q, k, v and o must be 16-byte aligned");
+    onionop::AttnArgs a{};
+    a.E = E; a.QL = QL; a.KL = KL; a.QH = QH; a.KH = KH; a.B = B;
+    a.q = q; a.k = k; a.v = v; a.pair = pair; a.kpad = kpad; a.causal = causal != 0; a.scale = scale;
+    a.o = o; a.ms = ms; a.ls = ls;
+    if (!onionop::launch_attn_fwd((hipStream_t)stream, dtype, a))
+        return fail(ONIONOP_E_UNSUPPORTED, "flash_attention: no kernel for %s E=%lld", dt_name(dtype), (long long)E);
+    return check_launch("flash_attention");
+}
+
+size_t onionop_flash_attn_bwd_workspace(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
+                                        int64_t B) {
+    (void)dtype; (void)E; (void)KL; (void)KH;
+    if (QL <= 0 || QH <= 0 || B <= 0) return 0;
+    const size_t rows = (size_t)QL * (size_t)QH * (size_t)B;
+    return 2 * rows * sizeof(float) + 256;  // lse2 and delta, each 256-byte aligned
+}
+
+// Shared body of the backward entry points; `stages` selects which kernels run.
+static int attn_bwd_common(const char* what, int stages, void* stream, int dtype, int64_t E, int64_t QL, int64_t KL,
+                           int64_t QH, int64_t KH, int64_t B, const void* dO, const void* o, const float* ms,
+                           const float* ls, const void* q, const void* k, const void* v, const void* pair,
+                           const uint8_t* kpad, int causal, float scale, int qk_fp16, void* dq, void* dk, void* dv,
+                           void* dpair, void* workspace, size_t workspace_bytes) {
+    int st = check_attn(dtype, E, QL, KL, QH, KH, B);
+    if (st) return st;
+    const bool any_q = QL * QH * B > 0, any_k = KL * KH * B > 0;
+    if (stages & onionop::kBwdPre) {
+        if (any_q && (!dO || !o || !ms || !ls)) return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);
+        if (!aligned16(dO) || !aligned16(o)) return fail(ONIONOP_E_SHAPE, "%s: tensors must be 16-byte aligned", what);
+    }
+    if (stages & (onionop::kBwdDkDv | onionop::kBwdDq)) {
+        if ((any_q && (!dO || !q)) || (any_k && (!k || !v)))
+            return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);
+        if (!aligned16(dO) || !aligned16(q) || !aligned16(k) || !aligned16(v))
+            return fail(ONIONOP_E_SHAPE, "%s: tensors must be 16-byte aligned", what);
+    }
+    if (stages & onionop::kBwdDkDv) {
+        if (any_k && (!dk || !dv)) return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);
+        if (!aligned16(dk) || !aligned16(dv)) return fail(ONIONOP_E_SHAPE, "%s: tensors must be 16-byte aligned", what);
+    }
+    if (stages & onionop::kBwdDq) {
+        if ((pair == nullptr) != (dpair == nullptr))
+            return fail(ONIONOP_E_NULL, "%s: dpair must be given exactly when pair is given", what);
+        if (any_q && !dq) return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);
+        if (!aligned16(dq)) return fail(ONIONOP_E_SHAPE, "%s: tensors must be 16-byte aligned", what);
+    }
+    const size_t need = onionop_flash_attn_bwd_workspace(dtype, E, QL, KL, QH, KH, B);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(ONIONOP_E_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", what, need, workspace_bytes);
+    onionop::AttnArgs a{};
+    a.E = E; a.QL = QL; a.KL = KL; a.QH = QH; a.KH = KH; a.B = B;
+    a.q = q; a.k = k; a.v = v; a.pair = pair; a.kpad = kpad; a.causal = causal != 0; a.scale = scale;
+    a.dO = dO; a.o_in = o; a.ms_in = ms; a.ls_in = ls; a.qk_fp16 = qk_fp16 != 0;
+    a.dq = dq; a.dk = dk; a.dv = dv; a.dpair = dpair;
+    if (need > 0) {
+        uintptr_t base = (reinterpret_cast<uintptr_t>(workspace) + 255) & ~uintptr_t(255);
+        const size_t rows = (size_t)QL * (size_t)QH * (size_t)B;
+        a.lse2 = reinterpret_cast<float*>(base);
+        a.delta = a.lse2 + rows;
+    }
+    if (!onionop::launch_attn_bwd((hipStream_t)stream, dtype, a, stages))
+        return fail(ONIONOP_E_UNSUPPORTED, "%s: no kernel for %s E=%lld", what, dt_name(dtype), (long long)E);
+    return check_launch(what);
+}
+
+int onionop_flash_attn_bwd(void* stream, int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
+                           int64_t B, const void* dO, const void* o, const float* ms, const float* ls,
+                           const void* q, const void* k, const void* v, const void* pair, const uint8_t* kpad,
+                           int causal, float scale, int qk_fp16, void* dq, void* dk, void* dv, void* dpair,
+                           void* workspace, size_t workspace_bytes) {
+    return attn_bwd_common("∇flash_attention", onionop::kBwdAll, stream, dtype, E, QL, KL, QH, KH, B, dO, o, ms, ls,
+                           q, k, v, pair, kpad, causal, scale, qk_fp16, dq, dk, dv, dpair, workspace,
+                           workspace_bytes);
+}
+
+int onionop_flash_attn_bwd_preprocess(void* stream, int dtype, int64_t E, int64_t QL, int64_t QH, int64_t B,
+                                      const void* dO, const void* o, const float* ms, const float* ls,
+                                      void* workspace, size_t workspace_bytes) {
+    return attn_bwd_common("∇flash_attention preprocess", onionop::kBwdPre, stream, dtype, E, QL, 0, QH, QH, B, dO,
+                           o, ms, ls, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 1.0f, 0, nullptr, nullptr,
+                           nullptr, nullptr, workspace, workspace_bytes);
+}
+
+int onionop_flash_attn_bwd_dkdv(void* stream, int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
+                                int64_t B, const void* dO, const void* q, const void* k, const void* v,
+                                const void* pair, const uint8_t* kpad, int causal, float scale, int qk_fp16,
+                                void* dk, void* dv, void* workspace, size_t workspace_bytes) {
+    return attn_bwd_common("∇flash_attention dK/dV", onionop::kBwdDkDv, stream, dtype, E, QL, KL, QH, KH, B, dO,
+                           nullptr, nullptr, nullptr, q, k, v, pair, kpad, causal, scale, qk_fp16, nullptr, dk, dv,
+                           nullptr, workspace, workspace_bytes);
+}
+
+int onionop_flash_attn_bwd_dq(void* stream, int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
+                              int64_t B, const void* dO, const void* q, const void* k, const void* v,
+                              const void* pair, const uint8_t* kpad, int causal, float scale, int qk_fp16,
+                              void* dq, void* dpair, void* workspace, size_t workspace_bytes) {
+    return attn_bwd_common("∇flash_attention dQ", onionop::kBwdDq, stream, dtype, E, QL, KL, QH, KH, B, dO, nullptr,
+                           nullptr, nullptr, q, k, v, pair, kpad, causal, scale, qk_fp16, dq, nullptr, nullptr,
+                           dpair, workspace, workspace_bytes);
+}
+
+// -------------------------------------------------------------------- softmax
+
+static int check_rows(const char* what, int dtype, int64_t n, int64_t rows) {
+    if (!valid_dt(dtype)) return fail(ONIONOP_E_DTYPE, "%s: unsupported element type code %d", what, dtype);
+    if (n < 0 || rows < 0) return fail(ONIONOP_E_SHAPE, "%s: negative dimension", what);
+    const int64_t vec = 16 / (int64_t)dt_size(dtype);
+    const int64_t lim = (n % vec == 0) ? onionop::max_row_elems(dtype) : 16 * 256;
+    if (n > lim)
+        return fail(ONIONOP_E_UNSUPPORTED, "%s: reduction length %lld exceeds the supported %lld", what,
+                    (long long)n, (long long)lim);
+    return ok();
+}
+
+int onionop_softmax_fwd(void* stream, int dtype, int64_t N, int64_t M, const void* x, void* y) {
+    int st = check_rows("online_softmax", dtype, N, M);
+    if (st) return st;
+    if (N * M > 0 && (!x || !y)) return fail(ONIONOP_E_NULL, "online_softmax: NULL tensor pointer");
+    if (!aligned16(x) || !aligned16(y)) return fail(ONIONOP_E_SHAPE, "online_softmax: tensors must be 16-byte aligned");
+    if (!onionop::launch_softmax_fwd((hipStream_t)stream, dtype, N, M, x, y))
+        return fail(ONIONOP_E_UNSUPPORTED, "online_softmax: no kernel for N=%lld", (long long)N);
+    return check_launch("online_softmax");
+}
+
+int onionop_softmax_bwd(void* stream, int dtype, int64_t N, int64_t M, const void* dy, const void* y, void* dx) {
+    int st = check_rows("∇online_softmax", dtype, N, M);
+    if (st) return st;
+    if (N * M > 0 && (!dy || !y || !dx)) return fail(ONIONOP_E_NULL, "∇online_softmax: NULL tensor pointer");
+    if (!aligned16(dy) || !aligned16(y) || !aligned16(dx))
+        return fail(ONIONOP_E_SHAPE, "∇online_softmax: tensors must be 16-byte aligned");
+    if (!onionop::launch_softmax_bwd((hipStream_t)stream, dtype, N, M, dy, y, dx))
+        return fail(ONIONOP_E_UNSUPPORTED, "∇online_softmax: no kernel for N=%lld", (long long)N);
+    return check_launch("∇online_softmax");
+}
+
+// ------------------------------------------------------------------- RMS norm
+
+int onionop_rms_norm_fwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n, const void* x,
+                         const void* w, float eps, float offset, void* y, float* rstd) {
+    int st = check_rows("rms_norm", dtype_x, emb, n);
+    if (st) return st;
+    if (!valid_dt(dtype_w)) return fail(ONIONOP_E_DTYPE, "rms_norm: unsupported weight type code %d", dtype_w);
+    if (emb * n > 0 && (!x || !w || !y || !rstd)) return fail(ONIONOP_E_NULL, "rms_norm: NULL tensor pointer");
+    if (n > 0 && emb > 0 && (!aligned16(x) || !aligned16(y)))
+        return fail(ONIONOP_E_SHAPE, "rms_norm: x and y must be 16-byte aligned");
+    if (n > 0 && emb == 0) return fail(ONIONOP_E_SHAPE, "rms_norm: empty embedding dimension");
+    if (!onionop::launch_rms_fwd((hipStream_t)stream, dtype_x, dtype_w, emb, n, x, w, eps, offset, y, rstd))
+        return fail(ONIONOP_E_UNSUPPORTED, "rms_norm: no kernel for emb=%lld", (long long)emb);
+    return check_launch("rms_norm");
+}
+
+size_t onionop_rms_norm_bwd_workspace(int64_t emb, int64_t n) {
+    if (emb <= 0 || n <= 0) return 0;
+    return (size_t)onionop::norm_bwd_groups(n) * (size_t)emb * sizeof(float);
+}
+
+int onionop_rms_norm_bwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n, const void* dy,
+                         const float* rstd, const void* x, const void* w, float offset, void* dx, float* dw,
+                         void* workspace, size_t workspace_bytes) {
+    int st = check_rows("∇rms_norm", dtype_x, emb, n);
+    if (st) return st;
+    if (!valid_dt(dtype_w)) return fail(ONIONOP_E_DTYPE, "∇rms_norm: unsupported weight type code %d", dtype_w);
+    if ((emb * n > 0 && (!dy || !rstd || !x || !dx)) || (emb > 0 && (!w || !dw)))
+        return fail(ONIONOP_E_NULL, "∇rms_norm: NULL tensor pointer");
+    if (n > 0 && emb > 0 && (!aligned16(dy) || !aligned16(x) || !aligned16(dx)))
+        return fail(ONIONOP_E_SHAPE, "∇rms_norm: dy, x and dx must be 16-byte aligned");
+    const size_t need = onionop_rms_norm_bwd_workspace(emb, n);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+        return fail(ONIONOP_E_WORKSPACE, "∇rms_norm: 16-byte aligned workspace of %zu bytes needed, %zu given", need,
+                    workspace_bytes);
+    if (!onionop::launch_rms_bwd((hipStream_t)stream, dtype_x, dtype_w, emb, n, dy, rstd, x, w, offset, dx, dw,
+                                 (float*)workspace))
+        return fail(ONIONOP_E_UNSUPPORTED, "∇rms_norm: no kernel for emb=%lld", (long long)emb);
+    return check_launch("∇rms_norm");
+}
+
+// ----------------------------------------------------------------- layer norm
+
+int onionop_layer_norm_fwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n, const void* x,
+                           const void* w, const void* b, float eps, void* y, float* mu, float* rstd) {
+    int st = check_rows("layer_norm", dtype_x, emb, n);
+    if (st) return st;
+    if (!valid_dt(dtype_w)) return fail(ONIONOP_E_DTYPE, "layer_norm: unsupported weight type code %d", dtype_w);
+    if (emb * n > 0 && (!x || !w || !b || !y || !mu || !rstd))
+        return fail(ONIONOP_E_NULL, "layer_norm: NULL tensor pointer");
+    if (n > 0 && emb > 0 && (!aligned16(x) || !aligned16(y)))
+        return fail(ONIONOP_E_SHAPE, "layer_norm: x and y must be 16-byte aligned");
+    if (n > 0 && emb == 0) return fail(ONIONOP_E_SHAPE, "layer_norm: empty embedding dimension");
+    if (!onionop::launch_ln_fwd((hipStream_t)stream, dtype_x, dtype_w, emb, n, x, w, b, eps, y, mu, rstd))
+        return fail(ONIONOP_E_UNSUPPORTED, "layer_norm: no kernel for emb=%lld", (long long)emb);
+    return check_launch("layer_norm");
+}
+
+size_t onionop_layer_norm_bwd_workspace(int64_t emb, int64_t n) {
+    if (emb <= 0 || n <= 0) return 0;
+    return 2 * (size_t)onionop::norm_bwd_groups(n) * (size_t)emb * sizeof(float);
+}
+
+int onionop_layer_norm_bwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n, const void* dy,
+                           const float* mu, const float* rstd, const void* x, const void* w, void* dx, void* dw,
+                           void* db, void* workspace, size_t workspace_bytes) {
+    int st = check_rows("∇layer_norm", dtype_x, emb, n);
+    if (st) return st;
+    if (!valid_dt(dtype_w)) return fail(ONIONOP_E_DTYPE, "∇layer_norm: unsupported weight type code %d", dtype_w);
+    if ((emb * n > 0 && (!dy || !mu || !rstd || !x || !dx)) || (emb > 0 && (!w || !dw || !db)))
+        return fail(ONIONOP_E_NULL, "∇layer_norm: NULL tensor pointer");
+    if (n > 0 && emb > 0 && (!aligned16(dy) || !aligned16(x) || !aligned16(dx)))
+        return fail(ONIONOP_E_SHAPE, "∇layer_norm: dy, x and dx must be 16-byte aligned");
+    const size_t need = onionop_layer_norm_bwd_workspace(emb, n);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+        return fail(ONIONOP_E_WORKSPACE, "∇layer_norm: 16-byte aligned workspace of %zu bytes needed, %zu given",
+                    need, workspace_bytes);
+    if (!onionop::launch_ln_bwd((hipStream_t)stream, dtype_x, dtype_w, emb, n, dy, mu, rstd, x, w, dx, dw, db,
+                                (float*)workspace))
+        return fail(ONIONOP_E_UNSUPPORTED, "∇layer_norm: no kernel for emb=%lld", (long long)emb);
+    return check_launch("∇layer_norm");
+}
+
+// ----------------------------------------------------------------------- RoPE
+
+int onionop_llama_rope(void* stream, int dtype, int64_t E, int64_t L, int64_t QH, int64_t KH, int64_t B,
+                       const void* q, const void* k, const float* cos, const float* sin, float sin_sign,
+                       void* q_out, void* k_out) {
+    if (!valid_dt(dtype)) return fail(ONIONOP_E_DTYPE, "llama_rope: unsupported element type code %d", dtype);
+    if (E < 0 || L < 0 || QH < 0 || KH < 0 || B < 0) return fail(ONIONOP_E_SHAPE, "llama_rope: negative dimension");
+    if (E % 2 != 0) return fail(ONIONOP_E_SHAPE, "llama_rope: head dim %lld must be even", (long long)E);
+    if (E > 512) return fail(ONIONOP_E_UNSUPPORTED, "llama_rope: head dim %lld > 512", (long long)E);
+    if (E * L * B == 0 || (QH == 0 && KH == 0)) return ok();
+    if (!cos || !sin || (QH > 0 && (!q || !q_out)) || (KH > 0 && (!k || !k_out)))
+        return fail(ONIONOP_E_NULL, "llama_rope: NULL tensor pointer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(q_out) || !aligned16(k_out))
+        return fail(ONIONOP_E_SHAPE, "llama_rope: q, k and outputs must be 16-byte aligned");
+    if (!onionop::launch_rope((hipStream_t)stream, dtype, E, L, QH, KH, B, q, k, cos, sin, sin_sign, q_out, k_out))
+        return fail(ONIONOP_E_UNSUPPORTED, "llama_rope: no kernel for E=%lld", (long long)E);
+    return check_launch("llama_rope");
+}
+
+}  // extern "C"

@@ -1,0 +1,104 @@
+// common.h -- shared device helpers for libonionop_hip.so (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace onionop {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+// 16-byte vector used for every coalesced global load / store.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+
+// float -> nearest float16 value, kept as float (used for the reference's Float16 Q/K).
+__device__ __forceinline__ float round_f16(float x) { return (float)(f16)x; }
+
+// Number of T elements in one 16-byte vector.
+template <typename T> struct Vec { static constexpr int N = 16 / sizeof(T); };
+
+// Load / store N = 16/sizeof(T) consecutive elements as float (16-byte aligned).
+template <typename T>
+__device__ __forceinline__ void load_vec(const T* __restrict__ p, float* out) {
+    union { u32x4 v; T e[Vec<T>::N]; } u;
+    u.v = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < Vec<T>::N; ++i) out[i] = to_f32(u.e[i]);
+}
+template <typename T>
+__device__ __forceinline__ void store_vec(T* __restrict__ p, const float* in) {
+    union { u32x4 v; T e[Vec<T>::N]; } u;
+#pragma unroll
+    for (int i = 0; i < Vec<T>::N; ++i) u.e[i] = from_f32<T>(in[i]);
+    *reinterpret_cast<u32x4*>(p) = u.v;
+}
+
+// Zero `bytes` bytes at p (any alignment); used instead of hipMemsetAsync so that the
+// library records only kernels when a caller captures it into a HIP graph.
+static __global__ void fill_zero_kernel(void* p, int64_t bytes) {
+    const int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    unsigned char* b = reinterpret_cast<unsigned char*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (i + j < bytes) b[i + j] = 0;
+}
+
+// ---------------------------------------------------------------- reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Block-wide sum of up to 16 waves; every thread gets the result.  `red` must hold
+// blockDim/64 floats of LDS.  Ends with the LDS free for reuse after the next barrier.
+template <int NWAVES>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    if (NWAVES == 1) return v;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NWAVES; ++i) t += red[i];
+    __syncthreads();
+    return t;
+}
+template <int NWAVES>
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    if (NWAVES == 1) return v;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float t = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NWAVES; ++i) t = fmaxf(t, red[i]);
+    __syncthreads();
+    return t;
+}
+
+}  // namespace onionop

@@ -1,0 +1,51 @@
+// launch.h -- internal launcher interface between the C ABI (abi.cpp) and the kernels.
+// Every launcher only enqueues on `s` and returns false for a configuration it has no
+// kernel for; validation happens in abi.cpp.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace onionop {
+
+struct AttnArgs {
+    int64_t E, QL, KL, QH, KH, B;
+    const void *q, *k, *v, *pair;
+    const uint8_t* kpad;
+    int causal;
+    float scale;
+    // forward
+    void* o;
+    float *ms, *ls;
+    // backward
+    const void *dO, *o_in;
+    const float *ms_in, *ls_in;
+    int qk_fp16;
+    void *dq, *dk, *dv, *dpair;
+    float *lse2, *delta;  // workspace: log2-domain log-sum-exp and rowsum(dO o), (B, QH, QL)
+};
+
+bool launch_attn_fwd(hipStream_t s, int dt, const AttnArgs& a);
+// stages: bit 0 = preprocess, bit 1 = dK/dV, bit 2 = dQ (+ dpair).
+enum { kBwdPre = 1, kBwdDkDv = 2, kBwdDq = 4, kBwdAll = 7 };
+bool launch_attn_bwd(hipStream_t s, int dt, const AttnArgs& a, int stages);
+
+bool launch_softmax_fwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* x, void* y);
+bool launch_softmax_bwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* dy, const void* y, void* dx);
+bool launch_rms_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* x, const void* w,
+                    float eps, float offset, void* y, float* rstd);
+bool launch_rms_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* dy, const float* rstd,
+                    const void* x, const void* w, float offset, void* dx, float* dw, float* ws);
+bool launch_ln_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* x, const void* w,
+                   const void* b, float eps, void* y, float* mu, float* rstd);
+bool launch_ln_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* dy, const float* mu,
+                   const float* rstd, const void* x, const void* w, void* dx, void* dw, void* db, float* ws);
+bool launch_rope(hipStream_t s, int dt, int64_t E, int64_t L, int64_t QH, int64_t KH, int64_t B, const void* q,
+                 const void* k, const float* cosv, const float* sinv, float sign, void* qo, void* ko);
+
+// Longest row (elements) the row-wise kernels keep in registers for dtype dt.
+int64_t max_row_elems(int dt);
+// Number of workgroups (= float32 partial rows in the workspace) of the norm backward.
+int64_t norm_bwd_groups(int64_t rows);
+
+}  // namespace onionop

@@ -1,0 +1,42 @@
+"""Tensor plumbing shared by the op modules: dtype codes, device checks, stream handle."""
+from __future__ import annotations
+
+import torch
+
+from ._lib import BF16, F16, F32
+
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+
+def dtype_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"{what}: unsupported element type {t.dtype} (float32, float16, bfloat16)") from None
+
+
+def device_tensor(t: torch.Tensor, what: str) -> torch.Tensor:
+    """Dense device tensor (the reference's dense arrays); no host fallback exists."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{what}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{what}: tensor must be on a ROCm device (got {t.device}); there is no CPU path")
+    return t.contiguous()
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def jdims(t: torch.Tensor) -> tuple:
+    """Shape as the reference's column-major Julia array would print it."""
+    return tuple(reversed(t.shape))
+
+
+def round_scalar(x: float, dtype: torch.dtype) -> float:
+    """x rounded to `dtype`, as the reference's T(x)."""
+    return float(torch.tensor(x, dtype=torch.float64).to(dtype).item())

@@ -1,0 +1,138 @@
+"""Flash attention: the host side of NNop.flash_attention over libonionop_hip.so.
+
+Shapes are the reference's column-major Julia arrays read as row-major torch tensors:
+  q (B, QH, QL, E)      == Julia (E, QL, QH, B)
+  k, v (B, KH, KL, E)   == Julia (E, KL, KH, B)
+  pair (B, KL, QL, QH)  == Julia (QH, QL, KL, B)   (additive bias, after the scale)
+  kpad_mask (B, KL)     == Julia (KL, B) Bool      (False = masked key)
+  ms, ls (B, QH, QL)    == Julia (QL, QH, B), float32
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._util import device_tensor, dtype_code, jdims, ptr, round_scalar, stream_of
+
+
+def _check_shapes(q, k, v, pair, kpad_mask):
+    """Validation of _flash_attention / ∇flash_attention (src/attention.jl:150-156,
+    src/attention_bwd.jl:221-227), with the reference's messages."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k and v must be 4-dimensional (E, L, H, B) arrays")
+    B, QH, QL, QE = q.shape
+    KB, KH, KL, KE = k.shape
+    if QE != KE:
+        raise ValueError(f"Embedding dim of Q `{QE}` must be the same as of K `{KE}`.")
+    if k.shape != v.shape:
+        raise ValueError(f"Shapes of K `{jdims(k)}` and V `{jdims(v)}` must be the same.")
+    if QE <= 0 or (QE & (QE - 1)) != 0:
+        raise ValueError("Only power-of-2 embedding dims are supported.")
+    if KH == 0 or QH % KH != 0:
+        raise ValueError(f"Number of query heads `{QH}` must be divisible by number of KV heads `{KH}`.")
+    if KB != B:
+        raise ValueError(f"Batch of Q `{B}` must be the same as of K `{KB}`.")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k and v must share one element type")
+    if pair is not None:
+        if tuple(pair.shape) != (B, KL, QL, QH):
+            raise ValueError(f"pair must have Julia shape {(QH, QL, KL, B)}, got {jdims(pair)}")
+        if pair.dtype != q.dtype:
+            raise TypeError("pair must have the element type of q")
+    if kpad_mask is not None:
+        if kpad_mask.dtype != torch.bool or tuple(kpad_mask.shape) != (B, KL):
+            raise ValueError(f"kpad_mask must be a Bool array of Julia shape {(KL, B)}")
+    return B, QH, QL, QE, KH, KL
+
+
+def attention_scale(E: int, dtype: torch.dtype) -> float:
+    """T(1/sqrt(E)) (src/attention.jl:166)."""
+    return round_scalar(1.0 / math.sqrt(E), dtype)
+
+
+def _flash_attention(q, k, v, pair=None, *, causal: bool, kpad_mask=None):
+    """Forward launcher; returns (o, ms, ls) like `_flash_attention` (src/attention.jl:145-197)."""
+    q = device_tensor(q, "flash_attention")
+    k = device_tensor(k, "flash_attention")
+    v = device_tensor(v, "flash_attention")
+    pair = None if pair is None else device_tensor(pair, "flash_attention")
+    kpad_mask = None if kpad_mask is None else device_tensor(kpad_mask, "flash_attention")
+    B, QH, QL, E, KH, KL = _check_shapes(q, k, v, pair, kpad_mask)
+    dt = dtype_code(q, "flash_attention")
+    o = torch.empty_like(q)
+    ms = torch.empty((B, QH, QL), dtype=torch.float32, device=q.device)
+    ls = torch.empty((B, QH, QL), dtype=torch.float32, device=q.device)
+    _lib.check(_lib.lib().onionop_flash_attn_fwd(
+        stream_of(q), dt, E, QL, KL, QH, KH, B, ptr(q), ptr(k), ptr(v), ptr(pair), ptr(kpad_mask),
+        int(bool(causal)), attention_scale(E, q.dtype), ptr(o), ptr(ms), ptr(ls)))
+    return o, ms, ls
+
+
+def grad_flash_attention(do, o, ms, ls, q, k, v, pair=None, *, causal: bool, kpad_mask=None,
+                         qk_fp16: bool = True):
+    """Backward launcher ∇flash_attention (src/attention_bwd.jl:213-303).
+
+    Returns (dq, dk, dv, dpair or None).  qk_fp16=True rounds Q and K to Float16 in every
+    product, as the reference does for every element type (src/attention_bwd.jl:20-21);
+    it only affects float32 inputs.
+    """
+    q = device_tensor(q, "∇flash_attention")
+    k = device_tensor(k, "∇flash_attention")
+    v = device_tensor(v, "∇flash_attention")
+    do = device_tensor(do, "∇flash_attention").to(q.dtype)
+    o = device_tensor(o, "∇flash_attention")
+    ms = device_tensor(ms, "∇flash_attention")
+    ls = device_tensor(ls, "∇flash_attention")
+    pair = None if pair is None else device_tensor(pair, "∇flash_attention")
+    kpad_mask = None if kpad_mask is None else device_tensor(kpad_mask, "∇flash_attention")
+    B, QH, QL, E, KH, KL = _check_shapes(q, k, v, pair, kpad_mask)
+    if do.shape != q.shape or o.shape != q.shape:
+        raise ValueError("Δ and o must have the shape of q")
+    dt = dtype_code(q, "∇flash_attention")
+    L = _lib.lib()
+    ws_bytes = L.onionop_flash_attn_bwd_workspace(dt, E, QL, KL, QH, KH, B)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dpair = None if pair is None else torch.empty_like(pair)
+    _lib.check(L.onionop_flash_attn_bwd(
+        stream_of(q), dt, E, QL, KL, QH, KH, B, ptr(do), ptr(o), ptr(ms), ptr(ls), ptr(q), ptr(k), ptr(v),
+        ptr(pair), ptr(kpad_mask), int(bool(causal)), attention_scale(E, q.dtype), int(bool(qk_fp16)), ptr(dq),
+        ptr(dk), ptr(dv), ptr(dpair), ptr(ws), int(ws_bytes)))
+    return dq, dk, dv, dpair
+
+
+class _FlashAttentionFn(torch.autograd.Function):
+    """The rrule of _flash_attention (src/attention_crc.jl:16-31)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, pair, kpad_mask, causal, qk_fp16):
+        o, ms, ls = _flash_attention(q, k, v, pair, causal=causal, kpad_mask=kpad_mask)
+        ctx.save_for_backward(q, k, v, pair, kpad_mask, o, ms, ls)
+        ctx.causal = causal
+        ctx.qk_fp16 = qk_fp16
+        ctx.mark_non_differentiable(ms, ls)
+        return o, ms, ls
+
+    @staticmethod
+    def backward(ctx, do, _dms, _dls):
+        q, k, v, pair, kpad_mask, o, ms, ls = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros_like(o)
+        dq, dk, dv, dpair = grad_flash_attention(do.contiguous(), o, ms, ls, q, k, v, pair, causal=ctx.causal,
+                                                 kpad_mask=kpad_mask, qk_fp16=ctx.qk_fp16)
+        return dq, dk, dv, dpair, None, None, None
+
+
+def flash_attention(q, k, v, pair: Optional[torch.Tensor] = None, *, causal: bool,
+                    kpad_mask: Optional[torch.Tensor] = None, qk_fp16: bool = True):
+    """NNop.flash_attention (src/attention_crc.jl:4-14): softmax(scale K^T Q + pair + masks) V.
+
+    Differentiable with torch autograd in q, k, v and pair; GQA when QH is a multiple of KH.
+    """
+    o, _, _ = _FlashAttentionFn.apply(q, k, v, pair, kpad_mask, bool(causal), bool(qk_fp16))
+    return o

@@ -1,0 +1,156 @@
+"""GPU parity of flash attention (fwd + bwd) against the oracle.
+
+Cases follow the reference sweeps (test/attention_tests.jl:6-18,
+test/causal_attention_tests.jl:6-16, test/gqa_attention_tests.jl:6-18): ragged and
+aligned lengths (255/256/257/511/512/1024), E in {16, 32, 64, 128}, pair bias, key
+padding with the last 11 keys of the last batch masked, GQA, causal.  Inputs are seeded
+N(0, 1) rounded to the dtype; the oracle runs in float64 on the same rounded values.
+Tolerance: norm-wise relative error <= 1e-5 (float32), <= 2e-2 (float16, bfloat16).
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import nnop
+import oracle
+from helpers import DTYPES, TOL, host, make, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(dev, dt, E, QL, KL, QH, KH, B, causal, use_pair, use_kpad, seed, qk16=False, kpad=None):
+    dtype = DTYPES[dt]
+    rng = np.random.default_rng(seed)
+    q, qn = make(rng, (B, QH, QL, E), dtype, dev)
+    k, kn = make(rng, (B, KH, KL, E), dtype, dev)
+    v, vn = make(rng, (B, KH, KL, E), dtype, dev)
+    do, don = make(rng, (B, QH, QL, E), dtype, dev)
+    pair = pairn = None
+    if use_pair:
+        pair, pairn = make(rng, (B, KL, QL, QH), dtype, dev)
+    kp = None
+    if use_kpad and kpad is None:
+        kpad = np.ones((B, KL), dtype=bool)
+        kpad[-1, -11:] = False
+    if kpad is not None:
+        kp = torch.from_numpy(kpad).to(dev)
+    print(f"case {dt} E={E} QL={QL} KL={KL} QH={QH} KH={KH} B={B} causal={causal} pair={use_pair} "
+          f"kpad={kpad is not None} seed={seed} qk16={qk16}", flush=True)
+    o, ms, ls = nnop._flash_attention(q, k, v, pair, causal=causal, kpad_mask=kp)
+    dq, dk, dv, dpair = nnop.grad_flash_attention(do, o, ms, ls, q, k, v, pair, causal=causal, kpad_mask=kp,
+                                                  qk_fp16=qk16)
+    torch.cuda.synchronize()
+    scale = nnop.attention_scale(E, dtype)
+    o_r, ms_r, ls_r = oracle.attn_fwd(qn, kn, vn, pairn, kpad, causal, scale)
+    dq_r, dk_r, dv_r, dp_r = oracle.attn_bwd(don, qn, kn, vn, pairn, kpad, causal, scale,
+                                            qk_fp16=qk16 and dtype == torch.float32)
+    tol = TOL[dtype]
+    errs = {"o": rel_err(host(o), o_r), "dq": rel_err(host(dq), dq_r), "dk": rel_err(host(dk), dk_r),
+            "dv": rel_err(host(dv), dv_r)}
+    if use_pair:
+        errs["dpair"] = rel_err(host(dpair), dp_r)
+    fin = np.isfinite(ms_r)
+    errs["ms"] = rel_err(host(ms)[fin], ms_r[fin]) if fin.any() else 0.0
+    errs["ls"] = rel_err(host(ls), ls_r)
+    assert np.all(host(ms)[~fin] == -np.inf) and np.all(host(ls)[~fin] == 0)
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"tolerance {tol}: {bad} (all: {errs})"
+    return errs
+
+
+CASES = [
+    # dt, E, QL, KL, QH, KH, B, causal, pair, kpad
+    ("f32", 16, 255, 255, 2, 2, 3, False, False, False),
+    ("f32", 32, 256, 511, 2, 2, 3, False, True, True),
+    ("f32", 64, 512, 256, 2, 2, 3, False, True, False),
+    ("f32", 64, 1024, 1024, 2, 2, 1, False, False, True),
+    ("f32", 128, 257, 257, 4, 2, 2, True, False, False),
+    ("f32", 64, 511, 511, 2, 2, 3, True, True, True),
+    ("f16", 16, 256, 256, 2, 2, 3, False, True, True),
+    ("f16", 32, 511, 255, 2, 2, 3, False, False, True),
+    ("f16", 64, 512, 512, 2, 2, 3, True, True, False),
+    ("f16", 64, 1024, 1024, 2, 2, 2, True, False, True),
+    ("f16", 128, 255, 512, 2, 2, 2, False, False, False),
+    ("bf16", 16, 255, 511, 2, 2, 3, False, True, False),
+    ("bf16", 32, 768, 768, 8, 8, 2, False, True, False),
+    ("bf16", 64, 1024, 1024, 4, 4, 2, True, False, False),
+    ("bf16", 64, 256, 256, 2, 2, 3, True, True, True),
+    ("bf16", 128, 512, 512, 4, 1, 2, True, False, False),
+    ("bf16", 128, 257, 257, 8, 2, 2, False, False, True),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(map(str, c)))
+def test_attention_parity(dev, case):
+    dt, E, QL, KL, QH, KH, B, causal, pair, kpad = case
+    run_case(dev, dt, E, QL, KL, QH, KH, B, causal, pair, kpad, seed=zlib.crc32(repr(case).encode()) % 1000)
+
+
+GQA = [(QH, KH, causal, E, L) for QH, KH in ((4, 1), (6, 2), (8, 2)) for causal in (False, True)
+       for E, L in ((32, 255), (64, 257))]
+
+
+@pytest.mark.parametrize("case", GQA, ids=lambda c: "-".join(map(str, c)))
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_gqa_parity(dev, dt, case):
+    QH, KH, causal, E, L = case
+    run_case(dev, dt, E, L, L, QH, KH, 2, causal, False, False, seed=7)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_fp32_qk_fp16_mode(dev, causal):
+    """The reference backward's Float16 Q/K (src/attention_bwd.jl:20-21), reproduced."""
+    run_case(dev, "f32", 64, 300, 300, 2, 2, 2, causal, True, False, seed=3, qk16=True)
+
+
+def test_fully_masked_rows(dev):
+    """A batch whose keys are all padded: o = 0, ms = -Inf, ls = 0 and finite gradients
+    (the reference gives NaN there)."""
+    kpad = np.ones((2, 130), dtype=bool)
+    kpad[1, :] = False
+    for dt in ("f32", "bf16"):
+        run_case(dev, dt, 32, 70, 130, 2, 2, 2, False, True, True, seed=5, kpad=kpad)
+
+
+def test_single_key(dev):
+    """L = 1: o = v exactly, whatever q."""
+    rng = np.random.default_rng(1)
+    q, _ = make(rng, (2, 2, 1, 64), torch.float32, dev)
+    k, _ = make(rng, (2, 2, 1, 64), torch.float32, dev)
+    v, _ = make(rng, (2, 2, 1, 64), torch.float32, dev)
+    o, ms, ls = nnop._flash_attention(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert torch.allclose(o, v, rtol=1e-6, atol=1e-6)
+    assert torch.all(ls == 1.0)
+
+
+def test_autograd_matches_launchers(dev):
+    rng = np.random.default_rng(11)
+    q, _ = make(rng, (1, 4, 200, 64), torch.bfloat16, dev)
+    k, _ = make(rng, (1, 2, 200, 64), torch.bfloat16, dev)
+    v, _ = make(rng, (1, 2, 200, 64), torch.bfloat16, dev)
+    qq, kk, vv = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    o = nnop.flash_attention(qq, kk, vv, causal=True)
+    o.sum().backward()
+    o2, ms, ls = nnop._flash_attention(q, k, v, causal=True)
+    dq, dk, dv, _ = nnop.grad_flash_attention(torch.ones_like(o2), o2, ms, ls, q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2)
+    assert torch.equal(qq.grad, dq) and torch.equal(kk.grad, dk) and torch.equal(vv.grad, dv)
+
+
+def test_errors_match_reference_messages(dev):
+    q = torch.zeros((1, 3, 8, 64), device=dev)
+    k = torch.zeros((1, 2, 8, 64), device=dev)
+    with pytest.raises(ValueError, match="Number of query heads `3` must be divisible by number of KV heads `2`."):
+        nnop.flash_attention(q, k, k, causal=False)
+    with pytest.raises(ValueError, match="Only power-of-2 embedding dims are supported."):
+        x = torch.zeros((1, 2, 8, 48), device=dev)
+        nnop.flash_attention(x, x, x, causal=False)
+    with pytest.raises(ValueError, match="must be the same as of K"):
+        nnop.flash_attention(torch.zeros((1, 2, 8, 32), device=dev), k, k, causal=False)
+    with pytest.raises(nnop.NNopError):
+        x = torch.zeros((1, 2, 8, 256), device=dev)
+        nnop.flash_attention(x, x, x, causal=False)
