@@ -567,8 +567,11 @@ void orc_attn_fwd(int mode, i64 E, i64 QL, i64 KL, i64 QH, i64 KH, i64 B, const 
 }
 
 /* EXACT backward: analytic gradients of o = P v with P = softmax(S), S = scale q.k + pair
- * + masks, in float64; with qk_fp16 the Q and K values are first rounded to float16.
- * dpair = dS (zero where masked). */
+ * + masks, in float64; dpair = dS (zero where masked).  With qk_fp16 it is the float64
+ * mathematics of the reference's backward: the row statistics (m, l) and o, hence
+ * delta = rowsum(dO o), come from the unrounded forward, while the recomputed scores,
+ * dK and dQ use Q and K rounded to float16 (src/attention_bwd.jl:20-21,88-92,197-210),
+ * so P = exp(S16 - m) / l is not renormalised. */
 static void attn_bwd_exact(i64 E, i64 QL, i64 KL, i64 QH, i64 KH, i64 B, const double* dO,
                            const double* q, const double* k, const double* v,
                            const double* pair, const uint8_t* kpad, int causal, double scale,
@@ -587,30 +590,44 @@ static void attn_bwd_exact(i64 E, i64 QL, i64 KL, i64 QH, i64 KH, i64 B, const d
     for (i64 b = 0; b < B; ++b)
         for (i64 kh = 0; kh < KH; ++kh) {
             double* s = (double*)malloc(sizeof(double) * (size_t)KL);
+            double* sf = (double*)malloc(sizeof(double) * (size_t)KL);
             double* dp = (double*)malloc(sizeof(double) * (size_t)KL);
+            double* orow = (double*)malloc(sizeof(double) * (size_t)E);
             for (i64 h = kh * rep; h < (kh + 1) * rep; ++h)
                 for (i64 i = 0; i < QL; ++i) {
                     double m = -INFINITY;
                     for (i64 j = 0; j < KL; ++j) {
-                        if (key_masked(causal, kpad, KL, i, j, b)) { s[j] = -INFINITY; continue; }
-                        double d = 0.0;
-                        for (i64 e = 0; e < E; ++e) d += qq[QIDX(e, i, h, b)] * kk[KIDX(e, j, kh, b)];
+                        if (key_masked(causal, kpad, KL, i, j, b)) { s[j] = sf[j] = -INFINITY; continue; }
+                        double d = 0.0, df = 0.0;
+                        for (i64 e = 0; e < E; ++e) {
+                            d += qq[QIDX(e, i, h, b)] * kk[KIDX(e, j, kh, b)];
+                            df += q[QIDX(e, i, h, b)] * k[KIDX(e, j, kh, b)];
+                        }
                         d *= scale;
-                        if (pair) d += pair[PIDX(h, i, j, b)];
+                        df *= scale;
+                        if (pair) { d += pair[PIDX(h, i, j, b)]; df += pair[PIDX(h, i, j, b)]; }
                         s[j] = d;
-                        if (d > m) m = d;
+                        sf[j] = df;
+                        if (df > m) m = df;
                     }
                     if (m == -INFINITY) continue;
+                    /* forward statistics and output from the unrounded scores */
                     double l = 0.0;
-                    for (i64 j = 0; j < KL; ++j) if (s[j] != -INFINITY) l += exp(s[j] - m);
+                    for (i64 j = 0; j < KL; ++j) if (sf[j] != -INFINITY) l += exp(sf[j] - m);
+                    for (i64 e = 0; e < E; ++e) orow[e] = 0.0;
+                    for (i64 j = 0; j < KL; ++j) {
+                        if (sf[j] == -INFINITY) continue;
+                        double p = exp(sf[j] - m) / l;
+                        for (i64 e = 0; e < E; ++e) orow[e] += p * v[KIDX(e, j, kh, b)];
+                    }
                     double delta = 0.0;
+                    for (i64 e = 0; e < E; ++e) delta += dO[QIDX(e, i, h, b)] * orow[e];
                     for (i64 j = 0; j < KL; ++j) {
                         if (s[j] == -INFINITY) { dp[j] = 0.0; s[j] = 0.0; continue; }
-                        s[j] = exp(s[j] - m) / l; /* P */
+                        s[j] = exp(s[j] - m) / l; /* P from the (possibly rounded) scores */
                         double d = 0.0;
                         for (i64 e = 0; e < E; ++e) d += dO[QIDX(e, i, h, b)] * v[KIDX(e, j, kh, b)];
                         dp[j] = d;
-                        delta += s[j] * d;
                     }
                     for (i64 j = 0; j < KL; ++j) {
                         double p = s[j];
@@ -625,7 +642,9 @@ static void attn_bwd_exact(i64 E, i64 QL, i64 KL, i64 QH, i64 KH, i64 B, const d
                     }
                 }
             free(s);
+            free(sf);
             free(dp);
+            free(orow);
         }
     free(qq);
     free(kk);

@@ -1,0 +1,106 @@
+"""The C ABI library and the host-side logic, without a GPU.
+
+* libonionop_hip.so loads and exports every entry point include/onionop.h declares,
+  with the ABI version the header states (no compute call is made here);
+* the Python signatures cover the same set;
+* host validation raises the reference's messages before any launch, and there is no
+  CPU fallback (host tensors are rejected).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import nnop
+from nnop import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "onionop.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(onionop_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_hot_path():
+    fns = header_functions()
+    for must in ("onionop_flash_attn_fwd", "onionop_flash_attn_bwd", "onionop_softmax_fwd", "onionop_softmax_bwd",
+                 "onionop_rms_norm_fwd", "onionop_rms_norm_bwd", "onionop_layer_norm_fwd", "onionop_layer_norm_bwd",
+                 "onionop_llama_rope"):
+        assert must in fns
+
+
+def test_library_exports_every_header_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [f for f in header_functions() if not hasattr(lib, f)]
+    assert not missing, missing
+    assert set(header_functions()) == set(_lib.SIGNATURES)
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define ONIONOP_ABI_VERSION (\d+)", open(HEADER).read())
+    assert int(m.group(1)) == nnop.lib().onionop_abi_version() == _lib.ABI_VERSION
+
+
+def test_workspace_queries_are_host_only():
+    L = nnop.lib()
+    assert L.onionop_flash_attn_bwd_workspace(2, 64, 4096, 4096, 4, 4, 4) >= 2 * 4096 * 16 * 4
+    assert L.onionop_flash_attn_bwd_workspace(2, 64, 0, 4096, 4, 4, 4) == 0
+    assert L.onionop_rms_norm_bwd_workspace(4096, 16384) == 1024 * 4096 * 4
+    assert L.onionop_layer_norm_bwd_workspace(4096, 3) == 2 * 3 * 4096 * 4
+
+
+def test_c_abi_validation_errors():
+    """Status codes and messages come back without touching a device (checks run first)."""
+    L = nnop.lib()
+    st = L.onionop_flash_attn_fwd(None, 2, 48, 8, 8, 2, 2, 1, None, None, None, None, None, 0, 1.0, None, None, None)
+    assert st == -1 and L.onionop_last_error() == b"Only power-of-2 embedding dims are supported."
+    st = L.onionop_flash_attn_fwd(None, 2, 64, 8, 8, 3, 2, 1, None, None, None, None, None, 0, 1.0, None, None, None)
+    assert st == -1 and b"must be divisible by number of KV heads" in L.onionop_last_error()
+    st = L.onionop_flash_attn_fwd(None, 7, 64, 8, 8, 2, 2, 1, None, None, None, None, None, 0, 1.0, None, None, None)
+    assert st == -2
+    st = L.onionop_flash_attn_fwd(None, 2, 256, 8, 8, 2, 2, 1, None, None, None, None, None, 0, 1.0, None, None, None)
+    assert st == -3
+    st = L.onionop_flash_attn_fwd(None, 2, 64, 8, 8, 2, 2, 1, None, None, None, None, None, 0, 1.0, None, None, None)
+    assert st == -5
+    st = L.onionop_flash_attn_bwd(None, 2, 64, 8, 8, 2, 2, 1, 16, 16, 16, 16, 16, 16, 16, 16, None, 0, 1.0, 0,
+                                  16, 16, 16, None, None, 0)
+    assert st == -5 and b"dpair" in L.onionop_last_error()
+    st = L.onionop_flash_attn_bwd(None, 2, 64, 8, 8, 2, 2, 1, 16, 16, 16, 16, 16, 16, 16, None, None, 0, 1.0, 0,
+                                  16, 16, 16, None, 16, 8)
+    assert st == -6
+    st = L.onionop_llama_rope(None, 2, 15, 4, 1, 1, 1, 16, 16, 16, 16, 1.0, 16, 16)
+    assert st == -1
+    st = L.onionop_softmax_fwd(None, 0, 1 << 20, 4, 16, 16)
+    assert st == -3
+
+
+def test_host_checks_use_reference_messages():
+    q = torch.zeros((1, 3, 8, 64))
+    k = torch.zeros((1, 2, 8, 64))
+    from nnop.attention import _check_shapes
+
+    with pytest.raises(ValueError, match=r"Number of query heads `3` must be divisible by number of KV heads `2`\."):
+        _check_shapes(q, k, k, None, None)
+    with pytest.raises(ValueError, match=r"Embedding dim of Q `32` must be the same as of K `64`\."):
+        _check_shapes(torch.zeros((1, 2, 8, 32)), k, k, None, None)
+    with pytest.raises(ValueError, match=r"Shapes of K `\(64, 8, 2, 1\)` and V `\(64, 9, 2, 1\)` must be the same\."):
+        _check_shapes(torch.zeros((1, 2, 8, 64)), k, torch.zeros((1, 2, 9, 64)), None, None)
+    with pytest.raises(ValueError, match=r"Only power-of-2 embedding dims are supported\."):
+        x = torch.zeros((1, 2, 8, 48))
+        _check_shapes(x, x, x, None, None)
+
+
+def test_no_cpu_fallback():
+    x = torch.zeros((4, 64))
+    with pytest.raises(ValueError, match="no CPU path"):
+        nnop.online_softmax(x)
+    with pytest.raises(ValueError, match="no CPU path"):
+        nnop.rms_norm(x, torch.ones(64))
+    q = torch.zeros((1, 2, 8, 64))
+    with pytest.raises(ValueError, match="no CPU path"):
+        nnop.flash_attention(q, q, q, causal=True)
