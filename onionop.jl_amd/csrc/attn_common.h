@@ -65,21 +65,35 @@ __device__ __forceinline__ typename Mfma<T>::frag load_frag(const T* p) {
     }
 }
 
-// Fragment at k positions kperm(c, h, j) = crow(KE*c + j, h) of a row stored contiguously
-// along k (row points at k = 0).  For KE = 8 these are two runs of 4: 16c + 4h + [0,4)
-// and 16c + 8 + 4h + [0,4); for KE = 1 it is the single element crow(c, h).
+// A fragment whose contraction index runs along the ROWS of a tile stored naturally,
+// X[k][m] (m contiguous, row stride S elements): the fragment holds rows m0 + l%32 of
+// X^T and k positions kb + kperm(c, h, j) = kb + crow(KE*c + j, h), the positions a C
+// tile reused as a B operand stands for.
+// 16-bit: two ds_read_b64_tr_b16.  Within each group of 16 lanes the instruction returns
+// to lane i the elements d[4r + i/4][i%4], r = 0..3, where d[j] are the four 16-bit values
+// at lane j's address; pointing lane 4r + q at X[k0 + r][mb + 4q] therefore gives lane i
+// the four consecutive k values X[k0 .. k0+3][mb + i].  Lane groups g = l/16 cover
+// m = m0 + 16*(g%2) + [0,16) and half h = g/2; the two reads fetch k0 = kb + 16c + 4h and
+// kb + 16c + 8 + 4h, matching kperm.  X must be in LDS and 8-byte aligned at each address.
+// float32: one element X[kb + crow(c, h)][m0 + l%32].
 template <typename T>
-__device__ __forceinline__ typename Mfma<T>::frag load_frag_kperm(const T* row, int c, int h) {
+__device__ __forceinline__ typename Mfma<T>::frag load_frag_tr(const T* X, int S, int m0, int kb, int c, int lane) {
     if constexpr (Mfma<T>::KE == 8) {
-        typedef T t4 __attribute__((ext_vector_type(4)));
-        const t4 lo = *reinterpret_cast<const t4*>(row + 16 * c + 4 * h);
-        const t4 hi = *reinterpret_cast<const t4*>(row + 16 * c + 8 + 4 * h);
-        typename Mfma<T>::frag f;
-        f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
-        f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
-        return f;
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+        const int g = lane >> 4, r = (lane >> 2) & 3, q = lane & 3, h = lane >> 5;
+        const int mb = m0 + 16 * (g & 1) + 4 * q;
+        const int k0 = kb + 16 * c + 4 * h + r;
+        const T* p0 = X + k0 * S + mb;
+        const T* p1 = p0 + 8 * S;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
+        union { s16x4 s[2]; typename Mfma<T>::frag f; } u;
+        u.s[0] = lo;
+        u.s[1] = hi;
+        return u.f;
     } else {
-        return row[crow(c, h)];
+        return X[(kb + crow(c, lane >> 5)) * S + m0 + (lane & 31)];
     }
 }
 

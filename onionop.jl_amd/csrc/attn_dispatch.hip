@@ -1,0 +1,56 @@
+// attn_dispatch.hip -- element-type dispatch of the attention launchers.
+#include "launch.h"
+
+namespace onionop {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+template <typename T> bool fwd_dispatch(hipStream_t s, const AttnArgs& a);
+template <typename T, bool QK16> bool bwd_dispatch(hipStream_t s, const AttnArgs& a, int stages);
+
+extern template bool fwd_dispatch<float>(hipStream_t, const AttnArgs&);
+extern template bool fwd_dispatch<f16>(hipStream_t, const AttnArgs&);
+extern template bool fwd_dispatch<bf16>(hipStream_t, const AttnArgs&);
+extern template bool bwd_dispatch<float, false>(hipStream_t, const AttnArgs&, int);
+extern template bool bwd_dispatch<float, true>(hipStream_t, const AttnArgs&, int);
+extern template bool bwd_dispatch<f16, false>(hipStream_t, const AttnArgs&, int);
+extern template bool bwd_dispatch<bf16, false>(hipStream_t, const AttnArgs&, int);
+
+static __global__ void zero_bytes_kernel(void* p, int64_t bytes) {
+    const int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    unsigned char* c = reinterpret_cast<unsigned char*>(p);
+    for (int j = 0; j < 4; ++j)
+        if (i + j < bytes) c[i + j] = 0;
+}
+
+bool launch_attn_fwd(hipStream_t s, int dt, const AttnArgs& a) {
+    if (a.QL == 0 || a.QH == 0 || a.B == 0) return true;
+    switch (dt) {
+        case 0: return fwd_dispatch<float>(s, a);
+        case 1: return fwd_dispatch<f16>(s, a);
+        case 2: return fwd_dispatch<bf16>(s, a);
+    }
+    return false;
+}
+
+bool launch_attn_bwd(hipStream_t s, int dt, const AttnArgs& a, int stages) {
+    if (a.B == 0 || a.QH == 0) return true;
+    if (a.QL == 0) {  // no queries: dk = dv = 0
+        if (!(stages & kBwdDkDv)) return true;
+        const int64_t bytes = (dt == 0 ? 4 : 2) * a.E * a.KL * a.KH * a.B;
+        if (bytes > 0) {
+            zero_bytes_kernel<<<dim3((unsigned)((bytes + 1023) / 1024)), dim3(256), 0, s>>>(a.dk, bytes);
+            zero_bytes_kernel<<<dim3((unsigned)((bytes + 1023) / 1024)), dim3(256), 0, s>>>(a.dv, bytes);
+        }
+        return true;
+    }
+    switch (dt) {
+        case 0: return a.qk_fp16 ? bwd_dispatch<float, true>(s, a, stages) : bwd_dispatch<float, false>(s, a, stages);
+        case 1: return bwd_dispatch<f16, false>(s, a, stages);
+        case 2: return bwd_dispatch<bf16, false>(s, a, stages);
+    }
+    return false;
+}
+
+}  // namespace onionop
