@@ -9,7 +9,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.normpath(os.path.join(_HERE, "..", "lib", "libonionop_hip.so"))
+# The in-tree build; ONIONOP_LIB may name another build of the same library.
+LIB_PATH = os.environ.get("ONIONOP_LIB") or os.path.normpath(os.path.join(_HERE, "..", "lib", "libonionop_hip.so"))
 
 F32, F16, BF16 = 0, 1, 2
 
