@@ -249,6 +249,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-memory", action="store_true", help="skip the HBM-bound kernel set")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run 3 plain device copies of MIB MiB (a known-size kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
@@ -291,6 +294,15 @@ def main():
                    "flop_convention": "14*B*H*L^2*E/2"},
         "roofline": roofline,
     }
+    if args.calibrate_copy > 0:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: calibration copies of {args.calibrate_copy} MiB done")
+        del src, dst
     if not args.no_memory:
         log("bench: HBM-bound kernels")
         result["memory_bound"] = memory_bound(torch, nnop, dev)

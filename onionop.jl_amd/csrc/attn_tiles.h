@@ -24,11 +24,17 @@ struct TileRegs {
     // Rows [r0, r0 + NR) of src (row length E); rows at or past nrows read as zero.
     template <bool QK16 = false>
     __device__ __forceinline__ void load(const T* __restrict__ src, int r0, int nrows) {
+        // Rows r0 .. r0 + NR - 1 are one contiguous run of NR * E elements; a tile wholly
+        // inside [0, nrows) (uniform across the workgroup) loads without per-vector checks.
+        const bool full = r0 + NR <= nrows;
+        const T* tile = src + (int64_t)r0 * E;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int vi = threadIdx.x + i * NT;
-            const int row = vi / VPR, e0 = (vi % VPR) * VN;
-            if (vi < NR * VPR && r0 + row < nrows) r[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + row) * E + e0);
+            const int row = vi / VPR;
+            const bool in_tile = (NR * VPR) % NT == 0 || vi < NR * VPR;
+            if (full && in_tile) r[i] = *reinterpret_cast<const u32x4*>(tile + vi * VN);
+            else if (in_tile && r0 + row < nrows) r[i] = *reinterpret_cast<const u32x4*>(tile + vi * VN);
             else r[i] = u32x4{0u, 0u, 0u, 0u};
             if constexpr (QK16 && sizeof(T) == 4) {
                 union { u32x4 v; float f[4]; } u;

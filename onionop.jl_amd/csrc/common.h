@@ -60,15 +60,33 @@ static __global__ void fill_zero_kernel(void* p, int64_t bytes) {
         if (i + j < bytes) b[i + j] = 0;
 }
 
+// 2^x by the hardware instruction (v_exp_f32), without the range reduction exp2f adds
+// for results below 2^-126; those may come back as 0, which softmax weights tolerate.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// max / sum over lanes l and l ^ 32, by v_permlane32_swap (no LDS round trip).  With
+// x in both operands the swap returns the low half broadcast to both halves and the
+// high half broadcast to both halves; every lane combines the two.
+__device__ __forceinline__ float pair32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ---------------------------------------------------------------- reductions
 __device__ __forceinline__ float wave_sum(float v) {
+    v = pair32_sum(v);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
     return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
+    v = pair32_max(v);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
     return v;
 }
 

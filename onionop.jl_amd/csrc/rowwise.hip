@@ -99,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void softmax_fwd_kernel(const T* __restri
             const bool ok = slot_valid<VEC>(n, i);
 #pragma unroll
             for (int j = 0; j < VEC; ++j) {
-                v[i][j] = exp2f(fmaf(v[i][j], kLog2e, -m2));
+                v[i][j] = fast_exp2(fmaf(v[i][j], kLog2e, -m2));
                 if (ok) s += v[i][j];
             }
         }
