@@ -57,6 +57,9 @@ int check_attn(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t
                     (long long)E);
     if (QL > (1LL << 30) || KL > (1LL << 30) || QH > 65535 || B > 65535)
         return fail(ONIONOP_E_UNSUPPORTED, "flash_attention: dimensions too large");
+    // The kernels address one (head, batch) slice of q/k/v with 32-bit byte offsets.
+    if ((QL > KL ? QL : KL) * E * (int64_t)dt_size(dtype) >= (1LL << 31))
+        return fail(ONIONOP_E_UNSUPPORTED, "flash_attention: sequence too long (L*E*sizeof(T) must be below 2^31 bytes)");
     return ok();
 }
 

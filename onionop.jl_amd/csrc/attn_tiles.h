@@ -14,6 +14,44 @@ namespace onionop {
 template <typename T, int EO> struct TileCfg { static constexpr int DS = EO + 8; };
 template <int EO> struct TileCfg<float, EO> { static constexpr int DS = EO + 1; };
 
+// Buffer resource over `bytes` bytes at `base`.  A buffer load whose VGPR byte offset
+// (plus the instruction offset) is at or past `bytes` returns zeros without touching
+// memory, so tail rows of a tile need no branches: every load is unconditional, which
+// also keeps the compiler's memory-counter waits exact across the software pipeline.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+// Waits until every outstanding vector-memory load has returned (s_waitcnt vmcnt(0)).
+// Issued once after the loads that precede a software-pipelined loop, so the compiler's
+// wait insertion does not carry them as possibly pending into the loop, where it would
+// otherwise wait on the loop's own prefetches before each use of those registers.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Resource over rows [0, nrows) of a row-major (rows x E) slice of T.
+template <typename T, int E>
+__device__ __forceinline__ rsrc_t slice_rsrc(const T* base, int nrows) {
+    return make_rsrc(base, (uint32_t)nrows * (uint32_t)(E * sizeof(T)));
+}
+// An MFMA fragment (KE consecutive elements) at element offset `elem` of a slice
+// resource; zero past the end of the slice.
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::frag bload_frag(rsrc_t r, uint32_t elem) {
+    if constexpr (Mfma<T>::KE == 8) {
+        union { u32x4 v; typename Mfma<T>::frag f; } u;
+        u.v = bload16(r, elem * (uint32_t)sizeof(T));
+        return u.f;
+    } else {
+        return bload_f32(r, elem * 4u);
+    }
+}
+
 template <typename T, int NR, int E, int NT>
 struct TileRegs {
     static constexpr int VN = 16 / (int)sizeof(T);  // elements per 16-byte vector
@@ -21,21 +59,16 @@ struct TileRegs {
     static constexpr int NV = (NR * VPR + NT - 1) / NT;
     u32x4 r[NV];
 
-    // Rows [r0, r0 + NR) of src (row length E); rows at or past nrows read as zero.
+    // Rows [r0, r0 + NR) of the slice behind `rs` (row length E); rows past the end of
+    // the slice read as zero.  Rows r0 .. r0 + NR - 1 are one contiguous run of NR * E
+    // elements, read as consecutive 16-byte vectors by consecutive threads.
     template <bool QK16 = false>
-    __device__ __forceinline__ void load(const T* __restrict__ src, int r0, int nrows) {
-        // Rows r0 .. r0 + NR - 1 are one contiguous run of NR * E elements; a tile wholly
-        // inside [0, nrows) (uniform across the workgroup) loads without per-vector checks.
-        const bool full = r0 + NR <= nrows;
-        const T* tile = src + (int64_t)r0 * E;
+    __device__ __forceinline__ void load(rsrc_t rs, int r0) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int vi = threadIdx.x + i * NT;
-            const int row = vi / VPR;
-            const bool in_tile = (NR * VPR) % NT == 0 || vi < NR * VPR;
-            if (full && in_tile) r[i] = *reinterpret_cast<const u32x4*>(tile + vi * VN);
-            else if (in_tile && r0 + row < nrows) r[i] = *reinterpret_cast<const u32x4*>(tile + vi * VN);
-            else r[i] = u32x4{0u, 0u, 0u, 0u};
+            const int vc = (NR * VPR) % NT == 0 || vi < NR * VPR ? vi : 0;  // idle threads re-read vector 0
+            r[i] = bload16(rs, ((uint32_t)r0 * E + (uint32_t)vc * VN) * (uint32_t)sizeof(T));
             if constexpr (QK16 && sizeof(T) == 4) {
                 union { u32x4 v; float f[4]; } u;
                 u.v = r[i];
@@ -50,7 +83,9 @@ struct TileRegs {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int vi = threadIdx.x + i * NT;
-            if (vi >= NR * VPR) continue;
+            if constexpr ((NR * VPR) % NT != 0) {
+                if (vi >= NR * VPR) continue;
+            }
             const int row = vi / VPR, e0 = (vi % VPR) * VN;
             if constexpr (sizeof(T) == 2) {
                 *reinterpret_cast<u32x4*>(dst + row * DS + e0) = r[i];
