@@ -62,11 +62,12 @@ struct TileRegs {
     // Rows [r0, r0 + NR) of the slice behind `rs` (row length E); rows past the end of
     // the slice read as zero.  Rows r0 .. r0 + NR - 1 are one contiguous run of NR * E
     // elements, read as consecutive 16-byte vectors by consecutive threads.
+    // `t` is this thread's index among the NT threads that share the tile.
     template <bool QK16 = false>
-    __device__ __forceinline__ void load(rsrc_t rs, int r0) {
+    __device__ __forceinline__ void load(rsrc_t rs, int r0, int t) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int vi = threadIdx.x + i * NT;
+            const int vi = t + i * NT;
             const int vc = (NR * VPR) % NT == 0 || vi < NR * VPR ? vi : 0;  // idle threads re-read vector 0
             r[i] = bload16(rs, ((uint32_t)r0 * E + (uint32_t)vc * VN) * (uint32_t)sizeof(T));
             if constexpr (QK16 && sizeof(T) == 4) {
@@ -79,10 +80,10 @@ struct TileRegs {
         }
     }
     // Write the tile to LDS dst[row * DS + e].
-    __device__ __forceinline__ void store(T* dst, int DS) const {
+    __device__ __forceinline__ void store(T* dst, int DS, int t) const {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int vi = threadIdx.x + i * NT;
+            const int vi = t + i * NT;
             if constexpr ((NR * VPR) % NT != 0) {
                 if (vi >= NR * VPR) continue;
             }
