@@ -255,7 +255,7 @@ int onionop_rms_norm_fwd(void* stream, int dtype_x, int dtype_w, int64_t emb, in
 
 size_t onionop_rms_norm_bwd_workspace(int64_t emb, int64_t n) {
     if (emb <= 0 || n <= 0) return 0;
-    return (size_t)onionop::norm_bwd_groups(n) * (size_t)emb * sizeof(float);
+    return (size_t)onionop::norm_bwd_ws_floats(n, emb) * sizeof(float);
 }
 
 int onionop_rms_norm_bwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n, const void* dy,
@@ -297,7 +297,7 @@ int onionop_layer_norm_fwd(void* stream, int dtype_x, int dtype_w, int64_t emb, 
 
 size_t onionop_layer_norm_bwd_workspace(int64_t emb, int64_t n) {
     if (emb <= 0 || n <= 0) return 0;
-    return 2 * (size_t)onionop::norm_bwd_groups(n) * (size_t)emb * sizeof(float);
+    return 2 * (size_t)onionop::norm_bwd_ws_floats(n, emb) * sizeof(float);
 }
 
 int onionop_layer_norm_bwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n, const void* dy,
@@ -329,6 +329,9 @@ int onionop_llama_rope(void* stream, int dtype, int64_t E, int64_t L, int64_t QH
     if (E < 0 || L < 0 || QH < 0 || KH < 0 || B < 0) return fail(ONIONOP_E_SHAPE, "llama_rope: negative dimension");
     if (E % 2 != 0) return fail(ONIONOP_E_SHAPE, "llama_rope: head dim %lld must be even", (long long)E);
     if (E > 512) return fail(ONIONOP_E_UNSUPPORTED, "llama_rope: head dim %lld > 512", (long long)E);
+    // The kernel addresses one (head, batch) slice with 32-bit byte offsets.
+    if (L * E * (int64_t)dt_size(dtype) >= (1LL << 31))
+        return fail(ONIONOP_E_UNSUPPORTED, "llama_rope: sequence too long (L*E*sizeof(T) must be below 2^31 bytes)");
     if (E * L * B == 0 || (QH == 0 && KH == 0)) return ok();
     if (!cos || !sin || (QH > 0 && (!q || !q_out)) || (KH > 0 && (!k || !k_out)))
         return fail(ONIONOP_E_NULL, "llama_rope: NULL tensor pointer");

@@ -14,20 +14,6 @@ namespace onionop {
 template <typename T, int EO> struct TileCfg { static constexpr int DS = EO + 8; };
 template <int EO> struct TileCfg<float, EO> { static constexpr int DS = EO + 1; };
 
-// Buffer resource over `bytes` bytes at `base`.  A buffer load whose VGPR byte offset
-// (plus the instruction offset) is at or past `bytes` returns zeros without touching
-// memory, so tail rows of a tile need no branches: every load is unconditional, which
-// also keeps the compiler's memory-counter waits exact across the software pipeline.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-}
-__device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
-}
 // Waits until every outstanding vector-memory load has returned (s_waitcnt vmcnt(0)).
 // Issued once after the loads that precede a software-pipelined loop, so the compiler's
 // wait insertion does not carry them as possibly pending into the loop, where it would

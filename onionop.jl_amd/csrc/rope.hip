@@ -29,13 +29,73 @@ __device__ __forceinline__ void store_n(T* __restrict__ p, const float* in) {
     }
 }
 
-// One thread = VP consecutive rotation pairs (i, i + E/2) of one position.
+// Rotates heads [0, H) of one position for one thread: x1 = x[i0 .. i0+VP),
+// x2 = x[half + i0 ..), with the loads of kU heads issued before any of their math so
+// that each thread keeps 2 kU 16-byte requests in flight.  Each (batch, head) slice is a
+// buffer resource of L*E elements (offsets fit 32 bits; heads past H read zero and drop
+// their stores, so the unrolled tail needs no branch).
+template <typename T, int VP>
+__device__ __forceinline__ void rope_heads(const T* x, T* xo, int64_t H, int64_t b, int64_t l, int64_t i0,
+                                           int64_t E, int64_t L, const float* c, const float* s) {
+    constexpr int kU = 4;
+    const int64_t half = E / 2;
+    const uint32_t slice = (uint32_t)(L * E * (int64_t)sizeof(T));
+    const uint32_t o1 = (uint32_t)((l * E + i0) * (int64_t)sizeof(T));
+    const uint32_t o2 = o1 + (uint32_t)(half * (int64_t)sizeof(T));
+    for (int64_t h0 = 0; h0 < H; h0 += kU) {
+        u32x4 a[kU], bb[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const bool ok = h0 + u < H;
+            const rsrc_t r = make_rsrc(x + ((b * H + (ok ? h0 + u : 0)) * L) * E, ok ? slice : 0u);
+            if constexpr (VP == Vec<T>::N) {
+                a[u] = bload16_nt(r, o1);
+                bb[u] = bload16_nt(r, o2);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const bool ok = h0 + u < H;
+            const int64_t base = ((b * H + (ok ? h0 + u : 0)) * L + l) * E + i0;
+            float x1[VP], x2[VP], y1[VP], y2[VP];
+            if constexpr (VP == Vec<T>::N) {
+                union { u32x4 v; T e[VP]; } u1, u2;
+                u1.v = a[u];
+                u2.v = bb[u];
+#pragma unroll
+                for (int j = 0; j < VP; ++j) { x1[j] = to_f32(u1.e[j]); x2[j] = to_f32(u2.e[j]); }
+            } else {
+                if (!ok) continue;
+                load_n<T, VP>(x + base, x1);
+                load_n<T, VP>(x + base + half, x2);
+            }
+#pragma unroll
+            for (int j = 0; j < VP; ++j) {
+                y1[j] = x1[j] * c[j] - x2[j] * s[j];
+                y2[j] = x2[j] * c[j] + x1[j] * s[j];
+            }
+            if constexpr (VP == Vec<T>::N) {
+                const rsrc_t r = make_rsrc(xo + ((b * H + (ok ? h0 + u : 0)) * L) * E, ok ? slice : 0u);
+                union { u32x4 v; T e[VP]; } w1, w2;
+#pragma unroll
+                for (int j = 0; j < VP; ++j) { w1.e[j] = from_f32<T>(y1[j]); w2.e[j] = from_f32<T>(y2[j]); }
+                bstore16_nt(w1.v, r, o1);
+                bstore16_nt(w2.v, r, o2);
+            } else {
+                store_n<T, VP>(xo + base, y1);
+                store_n<T, VP>(xo + base + half, y2);
+            }
+        }
+    }
+}
+
+// One thread = VP consecutive rotation pairs (i, i + E/2) of one position, for every q
+// head and then every k head.
 template <typename T, int VP>
 __global__ __launch_bounds__(256) void rope_kernel(const T* q, const T* k, const float* __restrict__ cosv,
                                                    const float* __restrict__ sinv, float sin_sign, T* qo, T* ko,
                                                    int64_t E, int64_t L, int64_t QH, int64_t KH, int64_t rows_per_wg,
                                                    int64_t tpr) {
-    const int64_t half = E / 2;
     const int64_t b = blockIdx.y;
     const int64_t l = (int64_t)blockIdx.x * rows_per_wg + threadIdx.x / tpr;
     const int64_t i0 = (threadIdx.x % tpr) * VP;
@@ -47,36 +107,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const T* q, const T* k, const
         c[j] = cosv[cs + j];
         s[j] = sinv[cs + j] * sin_sign;
     }
-    const int64_t H = QH > KH ? QH : KH;
-#pragma unroll 2
-    for (int64_t h = 0; h < H; ++h) {
-        if (h < QH) {
-            const int64_t base = ((b * QH + h) * L + l) * E + i0;
-            float x1[VP], x2[VP], y1[VP], y2[VP];
-            load_n<T, VP>(q + base, x1);
-            load_n<T, VP>(q + base + half, x2);
-#pragma unroll
-            for (int j = 0; j < VP; ++j) {
-                y1[j] = x1[j] * c[j] - x2[j] * s[j];
-                y2[j] = x2[j] * c[j] + x1[j] * s[j];
-            }
-            store_n<T, VP>(qo + base, y1);
-            store_n<T, VP>(qo + base + half, y2);
-        }
-        if (h < KH) {
-            const int64_t base = ((b * KH + h) * L + l) * E + i0;
-            float x1[VP], x2[VP], y1[VP], y2[VP];
-            load_n<T, VP>(k + base, x1);
-            load_n<T, VP>(k + base + half, x2);
-#pragma unroll
-            for (int j = 0; j < VP; ++j) {
-                y1[j] = x1[j] * c[j] - x2[j] * s[j];
-                y2[j] = x2[j] * c[j] + x1[j] * s[j];
-            }
-            store_n<T, VP>(ko + base, y1);
-            store_n<T, VP>(ko + base + half, y2);
-        }
-    }
+    rope_heads<T, VP>(q, qo, QH, b, l, i0, E, L, c, s);
+    rope_heads<T, VP>(k, ko, KH, b, l, i0, E, L, c, s);
 }
 
 template <typename T, int VP>

@@ -4,10 +4,17 @@
 // Layout: a Julia (N, M) column-major matrix is M contiguous rows of N elements here.
 // One 256-thread workgroup owns one row at a time and keeps the whole row in registers
 // (NV 16-byte vectors per thread), so every element is read from HBM once and written
-// once; reductions are wave64 shuffles plus one LDS exchange across the 4 waves.
-// Workgroups are persistent over rows (grid = min(rows, 8 x CUs)), so per-element
-// weights stay in registers and the backward's weight-gradient partials accumulate in
-// registers, one float32 partial row per workgroup, summed by a second small kernel.
+// once; reductions are wave64 shuffles plus one LDS exchange (one barrier) across the
+// 4 waves.  Workgroups are persistent over rows and software-pipelined: the loads of a
+// workgroup's next row are in flight while it reduces and stores the current one, so
+// reads and writes of neighbouring rows overlap and each thread keeps two rows of
+// requests outstanding.  Per-element weights stay in registers across rows, and the
+// backward's weight-gradient partials accumulate in registers, one float32 partial row
+// per workgroup, summed by a two-stage column reduction with a fixed order.
+// All row accesses are buffer loads / stores over a resource that ends at the row's
+// last element: tails read zero and drop their stores without branches.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -16,29 +23,57 @@ namespace onionop {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 
-// Element e of the row handled by (thread t, slot i) with VEC elements per vector:
-// vector index t + i*256 covers elements [VEC*(t + i*256), +VEC).
+// Row I/O for VEC elements of T per slot: slot i of thread t covers elements
+// [VEC (t + 256 i), +VEC).  VEC is 16 / sizeof(T) (one 16-byte vector) or 1.
 template <typename T, int VEC>
-__device__ __forceinline__ void load_row(const T* __restrict__ row, int64_t n, int i, float* out) {
-    const int64_t e0 = (int64_t)VEC * (threadIdx.x + (int64_t)i * kThreads);
-    if constexpr (VEC == Vec<T>::N) {
-        if (e0 < n) load_vec<T>(row + e0, out);
-        else {
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) out[j] = 0.f;
-        }
-    } else {
-        static_assert(VEC == 1, "scalar path");
-        out[0] = e0 < n ? to_f32(row[e0]) : 0.f;
+struct RowIO {
+    typedef typename std::conditional<VEC == 1, uint32_t, u32x4>::type raw;
+    static __device__ __forceinline__ uint32_t off(int i) {
+        return (uint32_t)(VEC * (threadIdx.x + i * kThreads)) * (uint32_t)sizeof(T);
     }
+    static __device__ __forceinline__ raw load(rsrc_t r, int i) {
+        if constexpr (VEC != 1) return bload16_nt(r, off(i));
+        else if constexpr (sizeof(T) == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off(i), 0, kNT);
+        else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off(i), 0, kNT);
+    }
+    static __device__ __forceinline__ void to_float(raw v, float* out) {
+        if constexpr (VEC != 1) {
+            union { u32x4 v; T e[VEC]; } u;
+            u.v = v;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) out[j] = to_f32(u.e[j]);
+        } else if constexpr (sizeof(T) == 4) {
+            out[0] = __uint_as_float(v);
+        } else {
+            union { uint16_t s; T e; } u;
+            u.s = (uint16_t)v;
+            out[0] = to_f32(u.e);
+        }
+    }
+    static __device__ __forceinline__ void store(rsrc_t r, int i, const float* in) {
+        if constexpr (VEC != 1) {
+            union { u32x4 v; T e[VEC]; } u;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) u.e[j] = from_f32<T>(in[j]);
+            bstore16_nt(u.v, r, off(i));
+        } else if constexpr (sizeof(T) == 4) {
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(in[0]), r, (int)off(i), 0, kNT);
+        } else {
+            union { uint16_t s; T e; } u;
+            u.e = from_f32<T>(in[0]);
+            __builtin_amdgcn_raw_buffer_store_b16(u.s, r, (int)off(i), 0, kNT);
+        }
+    }
+};
+
+// Resource over row r of a (rows x n) matrix; an empty one for r >= rows (its loads
+// read zero), so the prefetch of a row past the end needs no branch.
+template <typename T>
+__device__ __forceinline__ rsrc_t row_rsrc(const T* base, int64_t r, int64_t rows, int64_t n) {
+    const bool ok = r < rows;
+    return make_rsrc(base + (ok ? r : 0) * n, ok ? (uint32_t)(n * (int64_t)sizeof(T)) : 0u);
 }
-template <typename T, int VEC>
-__device__ __forceinline__ void store_row(T* __restrict__ row, int64_t n, int i, const float* in) {
-    const int64_t e0 = (int64_t)VEC * (threadIdx.x + (int64_t)i * kThreads);
-    if (e0 >= n) return;
-    if constexpr (VEC == Vec<T>::N) store_vec<T>(row + e0, in);
-    else row[e0] = from_f32<T>(in[0]);
-}
+
 template <int VEC>
 __device__ __forceinline__ bool slot_valid(int64_t n, int i) {
     return (int64_t)VEC * (threadIdx.x + (int64_t)i * kThreads) < n;
@@ -60,17 +95,46 @@ __device__ __forceinline__ void load_w(const void* __restrict__ w, int dt, int64
         out[j] = v;
     }
 }
-template <int VEC>
-__device__ __forceinline__ void store_w(void* __restrict__ w, int dt, int64_t n, int i, const float* in) {
-    const int64_t e0 = (int64_t)VEC * (threadIdx.x + (int64_t)i * kThreads);
+
+// Rows handled together per loop iteration: short rows (NV < 4 vectors per thread) are
+// processed R at a time, which halves (or quarters) the barriers per row and keeps more
+// bytes in flight per thread.
+template <int NV> struct RowsPerIter { static constexpr int R = NV >= 4 ? 1 : 4 / NV; };
+
+// Block-wide sums / max of K values with one barrier: the LDS slot alternates between
+// consecutive reductions (`par`), so a slot is rewritten only after every thread has
+// passed the barrier of the reduction in between, i.e. after it finished reading the
+// slot.  `red` holds 2 * kWaves * K floats.
+template <int K, bool MAX>
+__device__ __forceinline__ void block_reduce_n(float (&v)[K], float* red, int& par) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-        const int64_t e = e0 + j;
-        if (e < n) {
-            if (dt == 0) reinterpret_cast<float*>(w)[e] = in[j];
-            else if (dt == 1) reinterpret_cast<f16*>(w)[e] = from_f32<f16>(in[j]);
-            else reinterpret_cast<bf16*>(w)[e] = from_f32<bf16>(in[j]);
-        }
+    for (int k = 0; k < K; ++k) v[k] = MAX ? wave_max(v[k]) : wave_sum(v[k]);
+    float* slot = red + par * kWaves * K;
+    par ^= 1;
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) slot[k * kWaves + wid] = v[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        float t = slot[k * kWaves];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) t = MAX ? fmaxf(t, slot[k * kWaves + i]) : t + slot[k * kWaves + i];
+        v[k] = t;
+    }
+}
+
+// Loads rows rb R + k (k < R) of a (rows x n) matrix as raw slots (zero past the end).
+template <typename T, int VEC, int NV, int R>
+__device__ __forceinline__ void load_rows(const T* base, int64_t rb, int64_t rows, int64_t n,
+                                          typename RowIO<T, VEC>::raw (&out)[R][NV]) {
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const rsrc_t rs = row_rsrc(base, rb * R + k, rows, n);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) out[k][i] = RowIO<T, VEC>::load(rs, i);
     }
 }
 
@@ -79,38 +143,58 @@ __device__ __forceinline__ void store_w(void* __restrict__ w, int dt, int64_t n,
 template <typename T, int VEC, int NV>
 __global__ __launch_bounds__(kThreads) void softmax_fwd_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                                 int64_t n, int64_t rows) {
-    __shared__ float red[kWaves];
-    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-        const T* xr = x + r * n;
-        float v[NV][VEC];
+    typedef RowIO<T, VEC> IO;
+    constexpr int R = RowsPerIter<NV>::R;
+    __shared__ float red[2 * kWaves * R];
+    int par = 0;
+    const int64_t nblk = (rows + R - 1) / R;
+    typename IO::raw cur[R][NV], nxt[R][NV];
+    load_rows<T, VEC, NV, R>(x, blockIdx.x, rows, n, cur);
+    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
+        load_rows<T, VEC, NV, R>(x, rb + gridDim.x, rows, n, nxt);
+        float v[R][NV][VEC], m[R], sm[R];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) load_row<T, VEC>(xr, n, i, v[i]);
-        float m = -INFINITY;
+        for (int k = 0; k < R; ++k) {
+            m[k] = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < NV; ++i)
-            if (slot_valid<VEC>(n, i))
+            for (int i = 0; i < NV; ++i) {
+                IO::to_float(cur[k][i], v[k][i]);
+                if (slot_valid<VEC>(n, i))
 #pragma unroll
-                for (int j = 0; j < VEC; ++j) m = fmaxf(m, v[i][j]);
-        m = block_max<kWaves>(m, red);
-        const float m2 = m * kLog2e;
-        float s = 0.f;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const bool ok = slot_valid<VEC>(n, i);
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                v[i][j] = fast_exp2(fmaf(v[i][j], kLog2e, -m2));
-                if (ok) s += v[i][j];
+                    for (int j = 0; j < VEC; ++j) m[k] = fmaxf(m[k], v[k][i][j]);
             }
         }
-        s = block_sum<kWaves>(s, red);
-        const float inv = 1.0f / s;
+        block_reduce_n<R, true>(m, red, par);
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
+        for (int k = 0; k < R; ++k) {
+            const float m2 = m[k] * kLog2e;
+            sm[k] = 0.f;
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) v[i][j] *= inv;
-            store_row<T, VEC>(y + r * n, n, i, v[i]);
+            for (int i = 0; i < NV; ++i) {
+                const bool ok = slot_valid<VEC>(n, i);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    v[k][i][j] = fast_exp2(fmaf(v[k][i][j], kLog2e, -m2));
+                    if (ok) sm[k] += v[k][i][j];
+                }
+            }
         }
+        block_reduce_n<R, false>(sm, red, par);
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const float inv = 1.0f / sm[k];
+            const rsrc_t ry = row_rsrc(y, rb * R + k, rows, n);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) v[k][i][j] *= inv;
+                IO::store(ry, i, v[k][i]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) cur[k][i] = nxt[k][i];
     }
 }
 
@@ -118,26 +202,47 @@ __global__ __launch_bounds__(kThreads) void softmax_fwd_kernel(const T* __restri
 template <typename T, int VEC, int NV>
 __global__ __launch_bounds__(kThreads) void softmax_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ y,
                                                                 T* __restrict__ dx, int64_t n, int64_t rows) {
-    __shared__ float red[kWaves];
-    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-        float g[NV][VEC], yv[NV][VEC];
+    typedef RowIO<T, VEC> IO;
+    constexpr int R = RowsPerIter<NV>::R;
+    __shared__ float red[2 * kWaves * R];
+    int par = 0;
+    const int64_t nblk = (rows + R - 1) / R;
+    typename IO::raw cg[R][NV], cy[R][NV], ng[R][NV], ny[R][NV];
+    load_rows<T, VEC, NV, R>(dy, blockIdx.x, rows, n, cg);
+    load_rows<T, VEC, NV, R>(y, blockIdx.x, rows, n, cy);
+    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
+        load_rows<T, VEC, NV, R>(dy, rb + gridDim.x, rows, n, ng);
+        load_rows<T, VEC, NV, R>(y, rb + gridDim.x, rows, n, ny);
+        float g[R][NV][VEC], yv[R][NV][VEC], sd[R];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            load_row<T, VEC>(dy + r * n, n, i, g[i]);
-            load_row<T, VEC>(y + r * n, n, i, yv[i]);
+        for (int k = 0; k < R; ++k) {
+            sd[k] = 0.f;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                IO::to_float(cg[k][i], g[k][i]);
+                IO::to_float(cy[k][i], yv[k][i]);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) sd[k] = fmaf(g[k][i][j], yv[k][i][j], sd[k]);
+            }
         }
-        float s = 0.f;
+        block_reduce_n<R, false>(sd, red, par);
 #pragma unroll
-        for (int i = 0; i < NV; ++i)
+        for (int k = 0; k < R; ++k) {
+            const rsrc_t rx = row_rsrc(dx, rb * R + k, rows, n);
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) s = fmaf(g[i][j], yv[i][j], s);
-        s = block_sum<kWaves>(s, red);
+            for (int i = 0; i < NV; ++i) {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) g[i][j] = yv[i][j] * (g[i][j] - s);
-            store_row<T, VEC>(dx + r * n, n, i, g[i]);
+                for (int j = 0; j < VEC; ++j) g[k][i][j] = yv[k][i][j] * (g[k][i][j] - sd[k]);
+                IO::store(rx, i, g[k][i]);
+            }
         }
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                cg[k][i] = ng[k][i];
+                cy[k][i] = ny[k][i];
+            }
     }
 }
 
@@ -147,7 +252,10 @@ template <typename T, int VEC, int NV>
 __global__ __launch_bounds__(kThreads) void rms_fwd_kernel(const T* __restrict__ x, const void* __restrict__ w, int dtw,
                                                             T* __restrict__ y, float* __restrict__ rstd,
                                                             int64_t n, int64_t rows, float eps, float offset) {
-    __shared__ float red[kWaves];
+    typedef RowIO<T, VEC> IO;
+    constexpr int R = RowsPerIter<NV>::R;
+    __shared__ float red[2 * kWaves * R];
+    int par = 0;
     float wv[NV][VEC];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -156,24 +264,51 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_kernel(const T* __restrict__
         for (int j = 0; j < VEC; ++j) wv[i][j] += offset;
     }
     const float inv_n = 1.0f / (float)n;
-    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-        float v[NV][VEC];
+    const int64_t nblk = (rows + R - 1) / R;
+    typename IO::raw cur[R][NV], nxt[R][NV];
+    load_rows<T, VEC, NV, R>(x, blockIdx.x, rows, n, cur);
+    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
+        load_rows<T, VEC, NV, R>(x, rb + gridDim.x, rows, n, nxt);
+        float v[R][NV][VEC], ss[R];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) load_row<T, VEC>(x + r * n, n, i, v[i]);
-        float s = 0.f;
+        for (int k = 0; k < R; ++k) {
+            ss[k] = 0.f;
 #pragma unroll
-        for (int i = 0; i < NV; ++i)
+            for (int i = 0; i < NV; ++i) {
+                IO::to_float(cur[k][i], v[k][i]);
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) s = fmaf(v[i][j], v[i][j], s);
-        s = block_sum<kWaves>(s, red);
-        const float rs = 1.0f / sqrtf(s * inv_n + eps);
-        if (threadIdx.x == 0) rstd[r] = rs;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) v[i][j] = wv[i][j] * v[i][j] * rs;
-            store_row<T, VEC>(y + r * n, n, i, v[i]);
+                for (int j = 0; j < VEC; ++j) ss[k] = fmaf(v[k][i][j], v[k][i][j], ss[k]);
+            }
         }
+        block_reduce_n<R, false>(ss, red, par);
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const int64_t r = rb * R + k;
+            const float rs = 1.0f / sqrtf(ss[k] * inv_n + eps);
+            if (threadIdx.x == 0 && r < rows) rstd[r] = rs;
+            const rsrc_t ry = row_rsrc(y, r, rows, n);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) v[k][i][j] = wv[i][j] * v[k][i][j] * rs;
+                IO::store(ry, i, v[k][i]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) cur[k][i] = nxt[k][i];
+    }
+}
+
+// Float32 per-row statistic of rows rb R + k (0 past the end).
+template <int R>
+__device__ __forceinline__ void load_stats(const float* p, int64_t rb, int64_t rows, float (&out)[R]) {
+    const rsrc_t r = make_rsrc(p, (uint32_t)(rows * 4));
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const int64_t row = rb * R + k;
+        out[k] = bload_f32(r, row < rows ? (uint32_t)row * 4u : 0xFFFFFFF0u);
     }
 }
 
@@ -185,7 +320,10 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
                                                             const T* __restrict__ x, const void* __restrict__ w, int dtw,
                                                             float offset, T* __restrict__ dx, float* __restrict__ ws,
                                                             int64_t n, int64_t rows) {
-    __shared__ float red[kWaves];
+    typedef RowIO<T, VEC> IO;
+    constexpr int R = RowsPerIter<NV>::R;
+    __shared__ float red[2 * kWaves * R];
+    int par = 0;
     float wv[NV][VEC], dw[NV][VEC];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -194,39 +332,61 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
         for (int j = 0; j < VEC; ++j) { wv[i][j] += offset; dw[i][j] = 0.f; }
     }
     const float inv_n = 1.0f / (float)n;
-    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-        float g[NV][VEC], xv[NV][VEC];
+    const int64_t nblk = (rows + R - 1) / R;
+    typename IO::raw cg[R][NV], cx[R][NV], ng[R][NV], nx[R][NV];
+    float crs[R], nrs[R];
+    load_rows<T, VEC, NV, R>(dy, blockIdx.x, rows, n, cg);
+    load_rows<T, VEC, NV, R>(x, blockIdx.x, rows, n, cx);
+    load_stats<R>(rstd, blockIdx.x, rows, crs);
+    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
+        load_rows<T, VEC, NV, R>(dy, rb + gridDim.x, rows, n, ng);
+        load_rows<T, VEC, NV, R>(x, rb + gridDim.x, rows, n, nx);
+        load_stats<R>(rstd, rb + gridDim.x, rows, nrs);
+        float g[R][NV][VEC], xv[R][NV][VEC], dd[R];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            load_row<T, VEC>(dy + r * n, n, i, g[i]);
-            load_row<T, VEC>(x + r * n, n, i, xv[i]);
-        }
-        const float rs = rstd[r];
-        float dd = 0.f;
+        for (int k = 0; k < R; ++k) {
+            dd[k] = 0.f;
 #pragma unroll
-        for (int i = 0; i < NV; ++i)
+            for (int i = 0; i < NV; ++i) {
+                IO::to_float(cg[k][i], g[k][i]);
+                IO::to_float(cx[k][i], xv[k][i]);
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) dd = fmaf(g[i][j] * wv[i][j], xv[i][j], dd);
-        dd = block_sum<kWaves>(dd, red);
-        const float c = rs * rs * rs * dd * inv_n;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                dw[i][j] = fmaf(g[i][j], xv[i][j] * rs, dw[i][j]);
-                g[i][j] = rs * g[i][j] * wv[i][j] - c * xv[i][j];
+                for (int j = 0; j < VEC; ++j) dd[k] = fmaf(g[k][i][j] * wv[i][j], xv[k][i][j], dd[k]);
             }
-            store_row<T, VEC>(dx + r * n, n, i, g[i]);
+        }
+        block_reduce_n<R, false>(dd, red, par);
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const float rs = crs[k];  // 0 for rows past the end, whose g and x are 0 too
+            const float c3 = rs * rs * rs * dd[k] * inv_n;
+            const rsrc_t rx = row_rsrc(dx, rb * R + k, rows, n);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    dw[i][j] = fmaf(g[k][i][j], xv[k][i][j] * rs, dw[i][j]);
+                    g[k][i][j] = rs * g[k][i][j] * wv[i][j] - c3 * xv[k][i][j];
+                }
+                IO::store(rx, i, g[k][i]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                cg[k][i] = ng[k][i];
+                cx[k][i] = nx[k][i];
+            }
+            crs[k] = nrs[k];
         }
     }
-    float* wsr = ws + (int64_t)blockIdx.x * n;
+    const rsrc_t rw = make_rsrc(ws + (int64_t)blockIdx.x * n, (uint32_t)(n * 4));
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int64_t e0 = (int64_t)VEC * (threadIdx.x + (int64_t)i * kThreads);
+    for (int i = 0; i < NV; ++i)
 #pragma unroll
         for (int j = 0; j < VEC; ++j)
-            if (e0 + j < n) wsr[e0 + j] = dw[i][j];
-    }
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dw[i][j]), rw,
+                                                  (int)(((uint32_t)VEC * (threadIdx.x + i * kThreads) + j) * 4u), 0, 0);
 }
 
 // ------------------------------------------------------------------ layer norm
@@ -237,7 +397,10 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ 
                                                            const void* __restrict__ b, int dtw, T* __restrict__ y,
                                                            float* __restrict__ mu, float* __restrict__ rstd,
                                                            int64_t n, int64_t rows, float eps) {
-    __shared__ float red[kWaves];
+    typedef RowIO<T, VEC> IO;
+    constexpr int R = RowsPerIter<NV>::R;
+    __shared__ float red[2 * kWaves * R];
+    int par = 0;
     float wv[NV][VEC], bv[NV][VEC];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -245,35 +408,56 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ 
         load_w<VEC>(b, dtw, n, i, bv[i]);
     }
     const float inv_n = 1.0f / (float)n;
-    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-        float v[NV][VEC];
+    const int64_t nblk = (rows + R - 1) / R;
+    typename IO::raw cur[R][NV], nxt[R][NV];
+    load_rows<T, VEC, NV, R>(x, blockIdx.x, rows, n, cur);
+    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
+        load_rows<T, VEC, NV, R>(x, rb + gridDim.x, rows, n, nxt);
+        float v[R][NV][VEC], m[R], q[R];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) load_row<T, VEC>(x + r * n, n, i, v[i]);
-        float s = 0.f;
+        for (int k = 0; k < R; ++k) {
+            m[k] = 0.f;
 #pragma unroll
-        for (int i = 0; i < NV; ++i)
+            for (int i = 0; i < NV; ++i) {
+                IO::to_float(cur[k][i], v[k][i]);
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) s += v[i][j];
-        const float m = block_sum<kWaves>(s, red) * inv_n;
-        float q = 0.f;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const bool ok = slot_valid<VEC>(n, i);
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                const int64_t e = (int64_t)VEC * (threadIdx.x + (int64_t)i * kThreads) + j;
-                const float c = v[i][j] - m;
-                if (ok && e < n) q = fmaf(c, c, q);
+                for (int j = 0; j < VEC; ++j) m[k] += v[k][i][j];
             }
         }
-        const float rs = 1.0f / sqrtf(block_sum<kWaves>(q, red) * inv_n + eps);
-        if (threadIdx.x == 0) { mu[r] = m; rstd[r] = rs; }
+        block_reduce_n<R, false>(m, red, par);
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
+        for (int k = 0; k < R; ++k) {
+            m[k] *= inv_n;
+            q[k] = 0.f;
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) v[i][j] = fmaf((v[i][j] - m) * rs, wv[i][j], bv[i][j]);
-            store_row<T, VEC>(y + r * n, n, i, v[i]);
+            for (int i = 0; i < NV; ++i) {
+                const bool ok = slot_valid<VEC>(n, i);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    const int64_t e = (int64_t)VEC * (threadIdx.x + (int64_t)i * kThreads) + j;
+                    const float c = v[k][i][j] - m[k];
+                    if (ok && e < n) q[k] = fmaf(c, c, q[k]);
+                }
+            }
         }
+        block_reduce_n<R, false>(q, red, par);
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const int64_t r = rb * R + k;
+            const float rs = 1.0f / sqrtf(q[k] * inv_n + eps);
+            if (threadIdx.x == 0 && r < rows) { mu[r] = m[k]; rstd[r] = rs; }
+            const rsrc_t ry = row_rsrc(y, r, rows, n);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) v[k][i][j] = fmaf((v[k][i][j] - m[k]) * rs, wv[i][j], bv[i][j]);
+                IO::store(ry, i, v[k][i]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) cur[k][i] = nxt[k][i];
     }
 }
 
@@ -285,7 +469,10 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
                                                            const float* __restrict__ rstd, const T* __restrict__ x,
                                                            const void* __restrict__ w, int dtw, T* __restrict__ dx,
                                                            float* __restrict__ ws, int64_t n, int64_t rows) {
-    __shared__ float red[2 * kWaves];
+    typedef RowIO<T, VEC> IO;
+    constexpr int R = RowsPerIter<NV>::R;
+    __shared__ float red[2 * kWaves * 2 * R];
+    int par = 0;
     float wv[NV][VEC], dw[NV][VEC], db[NV][VEC];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -294,81 +481,130 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
         for (int j = 0; j < VEC; ++j) dw[i][j] = db[i][j] = 0.f;
     }
     const float inv_n = 1.0f / (float)n;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-        float g[NV][VEC], xv[NV][VEC];
+    const int64_t nblk = (rows + R - 1) / R;
+    typename IO::raw cg[R][NV], cx[R][NV], ng[R][NV], nx[R][NV];
+    float cm[R], crs[R], nm[R], nrs[R];
+    load_rows<T, VEC, NV, R>(dy, blockIdx.x, rows, n, cg);
+    load_rows<T, VEC, NV, R>(x, blockIdx.x, rows, n, cx);
+    load_stats<R>(mu, blockIdx.x, rows, cm);
+    load_stats<R>(rstd, blockIdx.x, rows, crs);
+    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
+        load_rows<T, VEC, NV, R>(dy, rb + gridDim.x, rows, n, ng);
+        load_rows<T, VEC, NV, R>(x, rb + gridDim.x, rows, n, nx);
+        load_stats<R>(mu, rb + gridDim.x, rows, nm);
+        load_stats<R>(rstd, rb + gridDim.x, rows, nrs);
+        float g[R][NV][VEC], xv[R][NV][VEC], c12[2 * R];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            load_row<T, VEC>(dy + r * n, n, i, g[i]);
-            load_row<T, VEC>(x + r * n, n, i, xv[i]);
+        for (int k = 0; k < R; ++k) {
+            c12[2 * k] = c12[2 * k + 1] = 0.f;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                IO::to_float(cg[k][i], g[k][i]);
+                IO::to_float(cx[k][i], xv[k][i]);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    xv[k][i][j] = (xv[k][i][j] - cm[k]) * crs[k];  // xn (zero-padded slots give g = 0)
+                    const float wdy = wv[i][j] * g[k][i][j];
+                    c12[2 * k] = fmaf(wdy, xv[k][i][j], c12[2 * k]);
+                    c12[2 * k + 1] += wdy;
+                }
+            }
         }
-        const float m = mu[r], rs = rstd[r];
-        float c1 = 0.f, c2 = 0.f;
+        block_reduce_n<2 * R, false>(c12, red, par);
 #pragma unroll
-        for (int i = 0; i < NV; ++i)
+        for (int k = 0; k < R; ++k) {
+            const float c1 = c12[2 * k] * inv_n, c2 = c12[2 * k + 1] * inv_n, rs = crs[k];
+            const rsrc_t rx = row_rsrc(dx, rb * R + k, rows, n);
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                xv[i][j] = (xv[i][j] - m) * rs;  // xn (zero-padded slots give g = 0)
-                const float wdy = wv[i][j] * g[i][j];
-                c1 = fmaf(wdy, xv[i][j], c1);
-                c2 += wdy;
+            for (int i = 0; i < NV; ++i) {
+                float o[VEC];
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    o[j] = (wv[i][j] * g[k][i][j] - fmaf(xv[k][i][j], c1, c2)) * rs;
+                    dw[i][j] = fmaf(g[k][i][j], xv[k][i][j], dw[i][j]);
+                    db[i][j] += g[k][i][j];
+                }
+                IO::store(rx, i, o);
             }
-        c1 = wave_sum(c1);
-        c2 = wave_sum(c2);
-        if (lane == 0) { red[wid] = c1; red[kWaves + wid] = c2; }
-        __syncthreads();
-        c1 = 0.f;
-        c2 = 0.f;
+        }
 #pragma unroll
-        for (int i = 0; i < kWaves; ++i) { c1 += red[i]; c2 += red[kWaves + i]; }
-        __syncthreads();
-        c1 *= inv_n;
-        c2 *= inv_n;
+        for (int k = 0; k < R; ++k) {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            float o[VEC];
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                o[j] = (wv[i][j] * g[i][j] - fmaf(xv[i][j], c1, c2)) * rs;
-                dw[i][j] = fmaf(g[i][j], xv[i][j], dw[i][j]);
-                db[i][j] += g[i][j];
+            for (int i = 0; i < NV; ++i) {
+                cg[k][i] = ng[k][i];
+                cx[k][i] = nx[k][i];
             }
-            store_row<T, VEC>(dx + r * n, n, i, o);
+            cm[k] = nm[k];
+            crs[k] = nrs[k];
         }
     }
-    float* wsw = ws + (int64_t)blockIdx.x * n;
-    float* wsb = ws + ((int64_t)gridDim.x + blockIdx.x) * n;
+    const rsrc_t rw = make_rsrc(ws + (int64_t)blockIdx.x * n, (uint32_t)(n * 4));
+    const rsrc_t rb = make_rsrc(ws + ((int64_t)gridDim.x + blockIdx.x) * n, (uint32_t)(n * 4));
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int64_t e0 = (int64_t)VEC * (threadIdx.x + (int64_t)i * kThreads);
+    for (int i = 0; i < NV; ++i)
 #pragma unroll
-        for (int j = 0; j < VEC; ++j)
-            if (e0 + j < n) { wsw[e0 + j] = dw[i][j]; wsb[e0 + j] = db[i][j]; }
-    }
+        for (int j = 0; j < VEC; ++j) {
+            const int off = (int)(((uint32_t)VEC * (threadIdx.x + i * kThreads) + j) * 4u);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dw[i][j]), rw, off, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(db[i][j]), rb, off, 0, 0);
+        }
 }
 
-// out[e] = sum_g ws[g, e] for e < n (column sums of the [groups, n] partials), written
-// as float32 or as dtype `dt`; `count` partial matrices are reduced (dw, then db).
-__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ ws, int64_t groups, int64_t n,
-                                                     void* __restrict__ out0, void* __restrict__ out1, int dt) {
-    const int64_t e = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
-    const int part = threadIdx.x >> 6;  // 4 waves split the groups
-    const int which = blockIdx.y;
-    __shared__ float red[4][64];
+// ------------------------------------------------------------------ column sums
+// The weight gradients are column sums of `groups` float32 partial rows (one matrix per
+// gradient, `count` of them).  Stage 1: block (x, y, z) sums partial rows
+// [kColChunk y, +kColChunk) of matrix z for 256 columns into stage row y; stage 2 sums
+// the stage rows of each column in order and converts to the output type.  Both the
+// blocking and the order are fixed, so the bits do not depend on the device.
+constexpr int kColChunk = 16;
+
+__global__ __launch_bounds__(256) void colsum_stage1_kernel(const float* __restrict__ ws, int64_t groups, int64_t n,
+                                                            float* __restrict__ st, int64_t nst) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t g0 = (int64_t)blockIdx.y * kColChunk;
+    const int cnt = (int)(groups - g0 < kColChunk ? groups - g0 : kColChunk);
+    const rsrc_t r = make_rsrc(ws + (int64_t)blockIdx.z * groups * n, (uint32_t)(groups * n * 4));
+    // all kColChunk loads in flight at once; rows past `groups` or columns past n read 0
+    float v[kColChunk];
+#pragma unroll
+    for (int i = 0; i < kColChunk; ++i) {
+        const bool ok = i < cnt && e < n;
+        v[i] = bload_f32(r, ok ? (uint32_t)((g0 + i) * n + e) * 4u : 0xFFFFFFF0u);
+    }
+#pragma unroll
+    for (int w = 1; w < kColChunk; w *= 2)  // fixed pairwise tree
+#pragma unroll
+        for (int i = 0; i < kColChunk; i += 2 * w) v[i] += v[i + w];
+    if (e < n) st[((int64_t)blockIdx.z * nst + blockIdx.y) * n + e] = v[0];
+}
+
+// 64 columns per block; the 4 waves take stage rows w, w + 4, ... and combine in order.
+__global__ __launch_bounds__(256) void colsum_stage2_kernel(const float* __restrict__ st, int64_t nst, int64_t n,
+                                                            void* __restrict__ out0, void* __restrict__ out1, int dt) {
+    __shared__ float part[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const float* src = st + (int64_t)blockIdx.y * nst * n + e;
     float s = 0.f;
     if (e < n) {
-        const float* base = ws + (int64_t)which * groups * n;
-        for (int64_t g = part; g < groups; g += 4) s += base[g * n + e];
+        float a[8];
+        int64_t i = w;
+        for (; i + 28 < nst; i += 32) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[j] = src[(i + 4 * j) * n];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s += a[j];
+        }
+        for (; i < nst; i += 4) s += src[i * n];
     }
-    red[part][threadIdx.x & 63] = s;
+    part[w][lane] = s;
     __syncthreads();
-    if (part == 0 && e < n) {
-        s = red[0][threadIdx.x] + red[1][threadIdx.x] + red[2][threadIdx.x] + red[3][threadIdx.x];
-        void* out = which == 0 ? out0 : out1;
-        if (dt == 0) reinterpret_cast<float*>(out)[e] = s;
-        else if (dt == 1) reinterpret_cast<f16*>(out)[e] = from_f32<f16>(s);
-        else reinterpret_cast<bf16*>(out)[e] = from_f32<bf16>(s);
-    }
+    if (w != 0 || e >= n) return;
+    s = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+    void* out = blockIdx.y == 0 ? out0 : out1;
+    if (dt == 0) reinterpret_cast<float*>(out)[e] = s;
+    else if (dt == 1) reinterpret_cast<f16*>(out)[e] = from_f32<f16>(s);
+    else reinterpret_cast<bf16*>(out)[e] = from_f32<bf16>(s);
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -410,15 +646,25 @@ static bool dispatch_row(int64_t n, Args&&... args) {
     return false;  // row longer than 16 vectors per thread: not supported
 }
 
+// Persistent grid: up to 8 workgroups per CU, but at least two rows per workgroup when
+// there are enough rows, so that every workgroup overlaps one row's stores with the
+// next row's loads.
 static inline int64_t grid_rows(int64_t rows) {
-    const int64_t g = 8LL * num_cus();
+    int64_t g = 8LL * num_cus();
+    if (rows < 2 * g) g = rows >= 2 * num_cus() ? (rows + 1) / 2 : rows;
     return rows < g ? rows : g;
+}
+
+// Grid over row blocks of R rows.
+template <int NV>
+static inline int64_t grid_blocks(int64_t rows) {
+    return grid_rows((rows + RowsPerIter<NV>::R - 1) / RowsPerIter<NV>::R);
 }
 
 template <typename T, int VEC, int NV>
 struct SoftmaxFwd {
     static bool run(hipStream_t s, const void* x, void* y, int64_t n, int64_t rows) {
-        softmax_fwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_rows(rows)), dim3(kThreads), 0, s>>>(
+        softmax_fwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_blocks<NV>(rows)), dim3(kThreads), 0, s>>>(
             (const T*)x, (T*)y, n, rows);
         return true;
     }
@@ -426,7 +672,7 @@ struct SoftmaxFwd {
 template <typename T, int VEC, int NV>
 struct SoftmaxBwd {
     static bool run(hipStream_t s, const void* dy, const void* y, void* dx, int64_t n, int64_t rows) {
-        softmax_bwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_rows(rows)), dim3(kThreads), 0, s>>>(
+        softmax_bwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_blocks<NV>(rows)), dim3(kThreads), 0, s>>>(
             (const T*)dy, (const T*)y, (T*)dx, n, rows);
         return true;
     }
@@ -435,7 +681,7 @@ template <typename T, int VEC, int NV>
 struct RmsFwd {
     static bool run(hipStream_t s, const void* x, const void* w, int dtw, void* y, float* rstd, int64_t n,
                     int64_t rows, float eps, float offset) {
-        rms_fwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_rows(rows)), dim3(kThreads), 0, s>>>(
+        rms_fwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_blocks<NV>(rows)), dim3(kThreads), 0, s>>>(
             (const T*)x, w, dtw, (T*)y, rstd, n, rows, eps, offset);
         return true;
     }
@@ -453,7 +699,7 @@ template <typename T, int VEC, int NV>
 struct LnFwd {
     static bool run(hipStream_t s, const void* x, const void* w, const void* b, int dtw, void* y, float* mu,
                     float* rstd, int64_t n, int64_t rows, float eps) {
-        ln_fwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_rows(rows)), dim3(kThreads), 0, s>>>(
+        ln_fwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_blocks<NV>(rows)), dim3(kThreads), 0, s>>>(
             (const T*)x, w, b, dtw, (T*)y, mu, rstd, n, rows, eps);
         return true;
     }
@@ -485,6 +731,25 @@ int64_t max_row_elems(int dt) {
 // bits of dw/db, do not depend on the GPU model.
 int64_t norm_bwd_groups(int64_t rows) { return rows < 1024 ? rows : 1024; }
 
+static int64_t colsum_stage_rows(int64_t groups) { return (groups + kColChunk - 1) / kColChunk; }
+
+int64_t norm_bwd_ws_floats(int64_t rows, int64_t n) {
+    const int64_t g = norm_bwd_groups(rows);
+    return (g + colsum_stage_rows(g)) * n;
+}
+
+// Column sums of `count` partial matrices at ws ([count][groups][n]) into out0 / out1,
+// with the stage rows after them ([count][nst][n]).
+static void colsum(hipStream_t s, float* ws, int64_t groups, int64_t n, int count, void* out0, void* out1,
+                   int dt) {
+    const int64_t nst = colsum_stage_rows(groups);
+    float* st = ws + (int64_t)count * groups * n;
+    const unsigned cx = (unsigned)((n + 255) / 256);
+    colsum_stage1_kernel<<<dim3(cx, (unsigned)nst, (unsigned)count), dim3(256), 0, s>>>(ws, groups, n, st, nst);
+    colsum_stage2_kernel<<<dim3((unsigned)((n + 63) / 64), (unsigned)count), dim3(256), 0, s>>>(st, nst, n, out0,
+                                                                                               out1, dt);
+}
+
 bool launch_softmax_fwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* x, void* y) {
     if (rows == 0 || n == 0) return true;
     ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, SoftmaxFwd>(n, s, x, y, n, rows));
@@ -515,7 +780,7 @@ bool launch_rms_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, con
         fill_zero_kernel<<<dim3((unsigned)((n * 4 + 1023) / 1024)), dim3(256), 0, s>>>(dw, n * 4);
         return true;
     }
-    colsum_kernel<<<dim3((unsigned)((n + 63) / 64), 1), dim3(256), 0, s>>>(ws, groups, n, dw, nullptr, 0);
+    colsum(s, ws, groups, n, 1, dw, nullptr, 0);
     return true;
 }
 bool launch_ln_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* x, const void* w,
@@ -537,7 +802,7 @@ bool launch_ln_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, cons
     bool ok = false;
     ONIONOP_DT_SWITCH(dt, T, ok = dispatch_row<T, LnBwd>(n, s, dy, mu, rstd, x, w, dtw, dx, ws, groups, n, rows));
     if (!ok) return false;
-    colsum_kernel<<<dim3((unsigned)((n + 63) / 64), 2), dim3(256), 0, s>>>(ws, groups, n, dw, db, dtw);
+    colsum(s, ws, groups, n, 2, dw, db, dtw);
     return true;
 }
 
