@@ -105,6 +105,13 @@ __device__ __forceinline__ float pair32_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// max of three floats as one v_max3_f32 (scores are never NaN here).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // ---------------------------------------------------------------- reductions
 __device__ __forceinline__ float wave_sum(float v) {
     v = pair32_sum(v);
