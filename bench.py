@@ -3,8 +3,8 @@
 
 Headline workload (the `value`): flash attention forward + backward, bfloat16,
 (E, L, H, B) = (64, 4096, 4, 4), causal, q/k/v ~ N(0,1)/sqrt(E), dO = 1 (loss = sum(o)).
-One step = _flash_attention + ∇flash_attention (4 kernels: forward, backward preprocess,
-dK/dV, dQ), inputs resident in HBM.  FLOPs per step use the flash-attention convention
+One step = _flash_attention + ∇flash_attention through the C ABI (3 kernels: forward, dQ with
+the backward preprocess fused, dK/dV), inputs resident in HBM.  FLOPs per step use the flash-attention convention
 14 B H L^2 E / 2 (forward 4, backward 10, causal halves).
 
 Also reported (`memory_bound`): HBM GB/s of online softmax (f32, 8192 x 1024), RMS norm
@@ -92,11 +92,18 @@ class AttnStep:
                                                   p(self.v), None, None, self.causal, self.scale, 0, p(self.dq),
                                                   None, p(self.ws), self.wsb))
 
+    def bwd(self):
+        """The combined backward (the entry point the drop-in's rrule calls): dQ with the
+        preprocess fused, then dK/dV."""
+        p = self.ptr
+        self.chk(self.L.onionop_flash_attn_bwd(self.stream, 2, *self.dims, p(self.do), p(self.o), p(self.ms),
+                                               p(self.ls), p(self.q), p(self.k), p(self.v), None, None, self.causal,
+                                               self.scale, 0, p(self.dq), p(self.dk), p(self.dv), None, p(self.ws),
+                                               self.wsb))
+
     def step(self):
         self.fwd()
-        self.pre()
-        self.dkdv()
-        self.dq_()
+        self.bwd()
 
 
 def time_region(torch, fn, iters):

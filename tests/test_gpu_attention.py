@@ -154,3 +154,54 @@ def test_errors_match_reference_messages(dev):
     with pytest.raises(nnop.NNopError):
         x = torch.zeros((1, 2, 8, 256), device=dev)
         nnop.flash_attention(x, x, x, causal=False)
+
+
+@pytest.mark.parametrize("dt,E,L,QH,KH,causal,use_pair,use_kpad", [
+    ("bf16", 64, 300, 4, 2, True, False, False),
+    ("f16", 128, 257, 2, 2, True, False, True),
+    ("f32", 32, 200, 4, 4, False, True, True),
+])
+def test_staged_backward_matches_combined(dev, dt, E, L, QH, KH, causal, use_pair, use_kpad):
+    """The staged entry points (preprocess, dK/dV, dQ) and the combined backward (dQ with
+    the preprocess fused, then dK/dV) compute the same gradients."""
+    from nnop import _lib
+    from nnop._util import ptr
+
+    dtype = DTYPES[dt]
+    rng = np.random.default_rng(7)
+    B = 2
+    q, _ = make(rng, (B, QH, L, E), dtype, dev)
+    k, _ = make(rng, (B, KH, L, E), dtype, dev)
+    v, _ = make(rng, (B, KH, L, E), dtype, dev)
+    do, _ = make(rng, (B, QH, L, E), dtype, dev)
+    pair = make(rng, (B, L, L, QH), dtype, dev)[0] if use_pair else None
+    kp = None
+    if use_kpad:
+        kpad = np.ones((B, L), dtype=bool)
+        kpad[-1, -11:] = False
+        kp = torch.from_numpy(kpad).to(dev)
+    o, ms, ls = nnop._flash_attention(q, k, v, pair, causal=causal, kpad_mask=kp)
+    dq, dk, dv, dpair = nnop.grad_flash_attention(do, o, ms, ls, q, k, v, pair, causal=causal, kpad_mask=kp)
+    L_ = _lib.lib()
+    dtc = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
+    dims = (E, L, L, QH, KH, B)
+    wsb = int(L_.onionop_flash_attn_bwd_workspace(dtc, *dims))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    sc = nnop.attention_scale(E, dtype)
+    dq2, dk2, dv2 = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dpair2 = None if pair is None else torch.empty_like(pair)
+    _lib.check(L_.onionop_flash_attn_bwd_preprocess(s, dtc, E, L, QH, B, ptr(do), ptr(o), ptr(ms), ptr(ls),
+                                                    ptr(ws), wsb))
+    _lib.check(L_.onionop_flash_attn_bwd_dkdv(s, dtc, *dims, ptr(do), ptr(q), ptr(k), ptr(v), ptr(pair), ptr(kp),
+                                              int(causal), sc, 1, ptr(dk2), ptr(dv2), ptr(ws), wsb))
+    _lib.check(L_.onionop_flash_attn_bwd_dq(s, dtc, *dims, ptr(do), ptr(q), ptr(k), ptr(v), ptr(pair), ptr(kp),
+                                            int(causal), sc, 1, ptr(dq2), ptr(dpair2), ptr(ws), wsb))
+    torch.cuda.synchronize()
+    # delta is summed in a different order by the two paths: agreement to a few ulps
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    pairs = {"dq": (dq, dq2), "dk": (dk, dk2), "dv": (dv, dv2)}
+    if use_pair:
+        pairs["dpair"] = (dpair, dpair2)
+    errs = {n: rel_err(host(a), host(b)) for n, (a, b) in pairs.items()}
+    assert all(e <= tol for e in errs.values()), errs
