@@ -138,6 +138,19 @@ def stage_times(torch, step, iters):
     return {n: sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(iters)) / iters for j, n in enumerate(names)}
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` at this workload from the copy-calibrated
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in profiles/hbm_traffic.json
+    (bench.py cannot read hardware counters itself); None when not recorded."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)["kernels"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if rec is None else int(rec["bytes"])
+
+
 def memory_bound(torch, nnop, dev, reps=10):
     """GB/s of the HBM-bound kernels over buffer sets rotated past the 256 MB MALL."""
     from nnop import _lib
@@ -288,8 +301,8 @@ def main():
     ach = stage_flops[dom] / (stages[dom] * 1e-3) / 1e12
     log("  kernels (us): " + ", ".join(f"{n} {t * 1e3:.1f}" for n, t in stages.items()))
     roofline = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1), "peak": MI355X_BF16_DENSE_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / MI355X_BF16_DENSE_TFLOPS, 4), "traffic": None,
-                "avg_us": round(stages[dom] * 1e3, 2),
+                "unit": "TFLOP/s", "frac": round(ach / MI355X_BF16_DENSE_TFLOPS, 4),
+                "traffic": measured_traffic(dom), "avg_us": round(stages[dom] * 1e3, 2),
                 "kernel_us": {n: round(t * 1e3, 2) for n, t in stages.items()}}
 
     result = {
