@@ -86,6 +86,44 @@ struct TileRegs {
     }
 };
 
+// Direct global -> LDS staging of a 16-bit tile (buffer_load_dwordx4 ... lds): each
+// lane's 16 bytes land at the wave's LDS base + 16 * lane, so one instruction fills 64
+// consecutive 16-byte slots and no registers hold the tile in transit.  The padded layout
+// is kept (row stride DS = E + 8 elements = CPR + 1 slots): a lane whose slot is a row's
+// padding chunk, or whose row is past the slice, uses an offset past the resource's end
+// and so writes zeros without touching memory.  Completion is tracked by the vector-
+// memory counter: the waiting wave issues s_waitcnt vmcnt before the barrier that
+// publishes the tile.
+template <typename T, int NR, int E, int NT>
+struct TileDMA {
+    static_assert(sizeof(T) == 2 && TileCfg<T, E>::DS == E + 8, "16-bit tiles with one padding chunk per row");
+    static constexpr int CPR = E * 2 / 16;  // data chunks per row
+    static constexpr int SPR = CPR + 1;     // LDS slots per row
+    static constexpr int NS = NR * SPR;     // slots per tile
+    static constexpr int NI = (NS + NT - 1) / NT;
+
+    // Rows [r0, r0 + NR) of the slice behind `rs` into the LDS tile at dst; t is the
+    // thread's index among the NT threads that share the tile, wave = t / 64 (uniform).
+    __device__ __forceinline__ static void load(rsrc_t rs, int r0, T* dst, int t, int wave) {
+        typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int slot0 = i * NT + wave * 64;  // wave-uniform first slot of this instruction
+            if constexpr (NS % NT != 0) {
+                if (slot0 >= NS) continue;
+            }
+            const int slot = slot0 + (t & 63);
+            const int row = slot / SPR, ch = slot - row * SPR;
+            const uint32_t off = ch < CPR ? ((uint32_t)(r0 + row) * (uint32_t)(E * 2) + (uint32_t)ch * 16u) : 0xFFFFFFF0u;
+            lds_void* base = (lds_void*)(dst + slot0 * 8);
+            if constexpr (NS % 64 != 0) {
+                if (slot >= NS) continue;  // partial last instruction: its lanes past the tile stay idle
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, base, 16, (int)off, 0, 0, 0);
+        }
+    }
+};
+
 // Zero columns [E, DS) of two NR-row LDS tiles (the padding read as rows E..31 of a 32-row
 // MFMA block when E = 16).
 template <typename T, int NR, int E, int DS, int NT>
