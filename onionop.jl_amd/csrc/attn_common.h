@@ -110,6 +110,41 @@ __device__ __forceinline__ typename Mfma<T>::frag c_to_frag(const f32x16& acc, i
     }
 }
 
+// Key-padding bytes of the keys one lane holds in a 32-key C-tile block (rows
+// crow(r, h)): keys kb0 + 8 rg + 4 h + [0, 4), rg = 0..3, are 4 consecutive bytes, so
+// four dword loads cover them (past KL the resource, of KL bytes, reads 0 = padded).
+// A dword that straddles KL would read as zero as a whole, so rows whose length is not
+// a multiple of 4 load the bytes one by one (uniform branch).
+struct KpadBlock {
+    uint32_t d[4];
+    __device__ __forceinline__ void load(rsrc_t r, int kb0, int h, int KL) {
+        if ((KL & 3) == 0) {
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg)
+                d[rg] = __builtin_amdgcn_raw_buffer_load_b32(r, kb0 + 8 * rg + 4 * h, 0, 0);
+        } else {
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                uint32_t x = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    x |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, kb0 + 8 * rg + 4 * h + j, 0, 0) << (8 * j);
+                d[rg] = x;
+            }
+        }
+    }
+    // key of register r is a real key (non-zero byte)
+    __device__ __forceinline__ bool ok(int r) const { return ((d[r >> 2] >> (8 * (r & 3))) & 0xFFu) != 0u; }
+    // every key of this lane's 16 is real / none is
+    __device__ __forceinline__ bool all() const {
+        bool z = false;
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) z |= ((d[rg] - 0x01010101u) & ~d[rg] & 0x80808080u) != 0u;  // has a zero byte
+        return !z;
+    }
+    __device__ __forceinline__ bool none() const { return (d[0] | d[1] | d[2] | d[3]) == 0u; }
+};
+
 // Element type helpers for the float16-rounded Q/K of the reference backward.
 template <typename T, bool QK16>
 __device__ __forceinline__ T qk_round(T x) {
