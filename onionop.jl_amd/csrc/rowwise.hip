@@ -646,25 +646,42 @@ static bool dispatch_row(int64_t n, Args&&... args) {
     return false;  // row longer than 16 vectors per thread: not supported
 }
 
-// Persistent grid: up to 8 workgroups per CU, but at least two rows per workgroup when
-// there are enough rows, so that every workgroup overlaps one row's stores with the
-// next row's loads.
-static inline int64_t grid_rows(int64_t rows) {
-    int64_t g = 8LL * num_cus();
-    if (rows < 2 * g) g = rows >= 2 * num_cus() ? (rows + 1) / 2 : rows;
-    return rows < g ? rows : g;
+// Workgroups of kThreads threads of kernel `k` that fit on one CU at once.
+template <typename Kern>
+static int fit_per_cu(Kern k) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, kThreads, 0) != hipSuccess || nb < 1) nb = 1;
+    return nb;
 }
 
-// Grid over row blocks of R rows.
-template <int NV>
-static inline int64_t grid_blocks(int64_t rows) {
-    return grid_rows((rows + RowsPerIter<NV>::R - 1) / RowsPerIter<NV>::R);
+// Persistent grid over `blocks` row blocks whose iteration loads `iter_bytes` bytes.
+// Few long-lived workgroups stream best on MI355X: about 32 KiB of loads in flight per
+// CU (2 to 8 workgroups per CU, no more than fit at once, so none waits for a slot), and
+// the row blocks split evenly, so every workgroup runs the same number of iterations.
+static int64_t grid_rows(int64_t blocks, int64_t iter_bytes, int fit) {
+    int64_t wpc = (32 * 1024) / (iter_bytes > 0 ? iter_bytes : 1);
+    wpc = wpc < 2 ? 2 : wpc > 8 ? 8 : wpc;
+    if (wpc > fit) wpc = fit;
+    const int64_t g = wpc * num_cus();
+    if (blocks <= g) return blocks;
+    const int64_t it = (blocks + g - 1) / g;
+    return (blocks + it - 1) / it;
+}
+
+// Grid over row blocks of R rows of n elements of T, `ins` input rows each, for a
+// kernel of which `fit` workgroups fit on a CU.
+template <typename T, int NV>
+static unsigned grid_blocks(int fit, int64_t rows, int64_t n, int ins) {
+    constexpr int R = RowsPerIter<NV>::R;
+    return (unsigned)grid_rows((rows + R - 1) / R, (int64_t)ins * R * n * (int64_t)sizeof(T), fit);
 }
 
 template <typename T, int VEC, int NV>
 struct SoftmaxFwd {
     static bool run(hipStream_t s, const void* x, void* y, int64_t n, int64_t rows) {
-        softmax_fwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_blocks<NV>(rows)), dim3(kThreads), 0, s>>>(
+        const auto k = softmax_fwd_kernel<T, VEC, NV>;
+        static const int fit = fit_per_cu(k);
+        k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 1)), dim3(kThreads), 0, s>>>(
             (const T*)x, (T*)y, n, rows);
         return true;
     }
@@ -672,7 +689,9 @@ struct SoftmaxFwd {
 template <typename T, int VEC, int NV>
 struct SoftmaxBwd {
     static bool run(hipStream_t s, const void* dy, const void* y, void* dx, int64_t n, int64_t rows) {
-        softmax_bwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_blocks<NV>(rows)), dim3(kThreads), 0, s>>>(
+        const auto k = softmax_bwd_kernel<T, VEC, NV>;
+        static const int fit = fit_per_cu(k);
+        k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 2)), dim3(kThreads), 0, s>>>(
             (const T*)dy, (const T*)y, (T*)dx, n, rows);
         return true;
     }
@@ -681,7 +700,9 @@ template <typename T, int VEC, int NV>
 struct RmsFwd {
     static bool run(hipStream_t s, const void* x, const void* w, int dtw, void* y, float* rstd, int64_t n,
                     int64_t rows, float eps, float offset) {
-        rms_fwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_blocks<NV>(rows)), dim3(kThreads), 0, s>>>(
+        const auto k = rms_fwd_kernel<T, VEC, NV>;
+        static const int fit = fit_per_cu(k);
+        k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 1)), dim3(kThreads), 0, s>>>(
             (const T*)x, w, dtw, (T*)y, rstd, n, rows, eps, offset);
         return true;
     }
@@ -699,7 +720,9 @@ template <typename T, int VEC, int NV>
 struct LnFwd {
     static bool run(hipStream_t s, const void* x, const void* w, const void* b, int dtw, void* y, float* mu,
                     float* rstd, int64_t n, int64_t rows, float eps) {
-        ln_fwd_kernel<T, VEC, NV><<<dim3((unsigned)grid_blocks<NV>(rows)), dim3(kThreads), 0, s>>>(
+        const auto k = ln_fwd_kernel<T, VEC, NV>;
+        static const int fit = fit_per_cu(k);
+        k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 1)), dim3(kThreads), 0, s>>>(
             (const T*)x, w, b, dtw, (T*)y, mu, rstd, n, rows, eps);
         return true;
     }
@@ -727,14 +750,22 @@ int64_t max_row_elems(int dt) {
     return 16LL * kThreads * (16 / es);
 }
 
-// Fixed (device-independent) so the workspace size and the summation order, hence the
-// bits of dw/db, do not depend on the GPU model.
-int64_t norm_bwd_groups(int64_t rows) { return rows < 1024 ? rows : 1024; }
+// Partial-row groups (= workgroups) of the norm backward for rows of n elements.  A
+// function of the shape only, so the workspace size and the summation order, hence the
+// bits of dw/db, do not depend on the GPU model.  Rows of 4096 or more elements take 256
+// groups (one long-lived workgroup per CU of an MI355X, which streams best), shorter rows
+// 512 or 1024, keeping the loads in flight per CU about the same.
+int64_t norm_bwd_groups(int64_t rows, int64_t n) {
+    int64_t per = n > 0 ? 4096 / n : 4;
+    per = per < 1 ? 1 : per > 4 ? 4 : per;
+    const int64_t g = 256 * per;
+    return rows < g ? rows : g;
+}
 
 static int64_t colsum_stage_rows(int64_t groups) { return (groups + kColChunk - 1) / kColChunk; }
 
 int64_t norm_bwd_ws_floats(int64_t rows, int64_t n) {
-    const int64_t g = norm_bwd_groups(rows);
+    const int64_t g = norm_bwd_groups(rows, n);
     return (g + colsum_stage_rows(g)) * n;
 }
 
@@ -768,7 +799,7 @@ bool launch_rms_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, con
 }
 bool launch_rms_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* dy, const float* rstd,
                     const void* x, const void* w, float offset, void* dx, float* dw, float* ws) {
-    const int64_t groups = norm_bwd_groups(rows);
+    const int64_t groups = norm_bwd_groups(rows, n);
     if (rows > 0) {
         bool ok = false;
         ONIONOP_DT_SWITCH(dt, T,
@@ -791,7 +822,7 @@ bool launch_ln_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, cons
 }
 bool launch_ln_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* dy, const float* mu,
                    const float* rstd, const void* x, const void* w, void* dx, void* dw, void* db, float* ws) {
-    const int64_t groups = norm_bwd_groups(rows);
+    const int64_t groups = norm_bwd_groups(rows, n);
     if (n == 0) return true;
     if (rows == 0) {
         const int64_t bytes = (dtw == 0 ? 4 : 2) * n;
