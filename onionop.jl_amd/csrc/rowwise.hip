@@ -6,9 +6,9 @@
 // (NV 16-byte vectors per thread), so every element is read from HBM once and written
 // once; reductions are wave64 shuffles plus one LDS exchange (one barrier) across the
 // 4 waves.  Workgroups are persistent over rows and software-pipelined: the loads of a
-// workgroup's next row are in flight while it reduces and stores the current one, so
-// reads and writes of neighbouring rows overlap and each thread keeps two rows of
-// requests outstanding.  Per-element weights stay in registers across rows, and the
+// workgroup's next rows (the next two row blocks in the norm backward) are in flight
+// while it reduces and stores the current ones, so reads and writes of neighbouring rows
+// overlap.  Per-element weights stay in registers across rows, and the
 // backward's weight-gradient partials accumulate in registers, one float32 partial row
 // per workgroup, summed by a two-stage column reduction with a fixed order.
 // All row accesses are buffer loads / stores over a resource that ends at the row's
@@ -138,6 +138,26 @@ __device__ __forceinline__ void load_rows(const T* base, int64_t rb, int64_t row
     }
 }
 
+// Calls step(slot, rb) for this workgroup's row blocks rb = blockIdx.x + j gridDim.x, in
+// order, with slot = j % D a compile-time constant: D register slots of prefetched rows
+// are then addressed statically (moving an in-flight load's registers would wait for it).
+template <int S, int D, typename F>
+__device__ __forceinline__ bool run_slots(int64_t& rb, int64_t nblk, F& step) {
+    if constexpr (S == D) {
+        return true;
+    } else {
+        if (rb >= nblk) return false;
+        step(std::integral_constant<int, S>(), rb);
+        rb += gridDim.x;
+        return run_slots<S + 1, D>(rb, nblk, step);
+    }
+}
+template <int D, typename F>
+__device__ __forceinline__ void for_row_blocks(int64_t nblk, F&& step) {
+    int64_t rb = blockIdx.x;
+    while (run_slots<0, D>(rb, nblk, step)) {}
+}
+
 // ------------------------------------------------------------------ softmax
 // y = exp(x - max) / sum(exp(x - max)) per row (online_softmax!, src/softmax.jl:19-58).
 template <typename T, int VEC, int NV>
@@ -248,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void softmax_bwd_kernel(const T* __restri
 
 // ------------------------------------------------------------------ RMS norm
 // rstd = 1/sqrt(mean(x^2) + eps); y = (offset + w) x rstd (_rms_norm!, src/rms_norm.jl:3-38).
-template <typename T, int VEC, int NV>
+template <typename T, int VEC, int NV, int D>
 __global__ __launch_bounds__(kThreads) void rms_fwd_kernel(const T* __restrict__ x, const void* __restrict__ w, int dtw,
                                                             T* __restrict__ y, float* __restrict__ rstd,
                                                             int64_t n, int64_t rows, float eps, float offset) {
@@ -265,20 +285,24 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_kernel(const T* __restrict__
     }
     const float inv_n = 1.0f / (float)n;
     const int64_t nblk = (rows + R - 1) / R;
-    typename IO::raw cur[R][NV], nxt[R][NV];
-    load_rows<T, VEC, NV, R>(x, blockIdx.x, rows, n, cur);
-    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
-        load_rows<T, VEC, NV, R>(x, rb + gridDim.x, rows, n, nxt);
+    typename IO::raw buf[D][R][NV];
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_rows<T, VEC, NV, R>(x, blockIdx.x + (int64_t)d * gridDim.x, rows, n, buf[d]);
+    for_row_blocks<D>(nblk, [&](auto slot, int64_t rb) {
+        constexpr int sl = decltype(slot)::value;
         float v[R][NV][VEC], ss[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) IO::to_float(buf[sl][k][i], v[k][i]);
+        load_rows<T, VEC, NV, R>(x, rb + (int64_t)D * gridDim.x, rows, n, buf[sl]);
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             ss[k] = 0.f;
 #pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                IO::to_float(cur[k][i], v[k][i]);
+            for (int i = 0; i < NV; ++i)
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) ss[k] = fmaf(v[k][i][j], v[k][i][j], ss[k]);
-            }
         }
         block_reduce_n<R, false>(ss, red, par);
 #pragma unroll
@@ -294,11 +318,7 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_kernel(const T* __restrict__
                 IO::store(ry, i, v[k][i]);
             }
         }
-#pragma unroll
-        for (int k = 0; k < R; ++k)
-#pragma unroll
-            for (int i = 0; i < NV; ++i) cur[k][i] = nxt[k][i];
-    }
+    });
 }
 
 // Float32 per-row statistic of rows rb R + k (0 past the end).
@@ -315,7 +335,7 @@ __device__ __forceinline__ void load_stats(const float* p, int64_t rb, int64_t r
 // Per row: dd = sum(dy (w+off) x); dx = rstd dy (w+off) - rstd^3 dd x / n; the dw partial
 // sum(dy x rstd) over this workgroup's rows goes to ws[blockIdx.x, :]
 // (_∇rms_norm!, src/rms_norm.jl:43-115).
-template <typename T, int VEC, int NV>
+template <typename T, int VEC, int NV, int D>
 __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__ dy, const float* __restrict__ rstd,
                                                             const T* __restrict__ x, const void* __restrict__ w, int dtw,
                                                             float offset, T* __restrict__ dx, float* __restrict__ ws,
@@ -333,26 +353,38 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
     }
     const float inv_n = 1.0f / (float)n;
     const int64_t nblk = (rows + R - 1) / R;
-    typename IO::raw cg[R][NV], cx[R][NV], ng[R][NV], nx[R][NV];
-    float crs[R], nrs[R];
-    load_rows<T, VEC, NV, R>(dy, blockIdx.x, rows, n, cg);
-    load_rows<T, VEC, NV, R>(x, blockIdx.x, rows, n, cx);
-    load_stats<R>(rstd, blockIdx.x, rows, crs);
-    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
-        load_rows<T, VEC, NV, R>(dy, rb + gridDim.x, rows, n, ng);
-        load_rows<T, VEC, NV, R>(x, rb + gridDim.x, rows, n, nx);
-        load_stats<R>(rstd, rb + gridDim.x, rows, nrs);
-        float g[R][NV][VEC], xv[R][NV][VEC], dd[R];
+    typename IO::raw bg[D][R][NV], bx[D][R][NV];
+    float brs[D][R];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const int64_t b0 = blockIdx.x + (int64_t)d * gridDim.x;
+        load_rows<T, VEC, NV, R>(dy, b0, rows, n, bg[d]);
+        load_rows<T, VEC, NV, R>(x, b0, rows, n, bx[d]);
+        load_stats<R>(rstd, b0, rows, brs[d]);
+    }
+    for_row_blocks<D>(nblk, [&](auto slot, int64_t rb) {
+        constexpr int sl = decltype(slot)::value;
+        float g[R][NV][VEC], xv[R][NV][VEC], dd[R], crs[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            crs[k] = brs[sl][k];
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                IO::to_float(bg[sl][k][i], g[k][i]);
+                IO::to_float(bx[sl][k][i], xv[k][i]);
+            }
+        }
+        const int64_t nb = rb + (int64_t)D * gridDim.x;
+        load_rows<T, VEC, NV, R>(dy, nb, rows, n, bg[sl]);
+        load_rows<T, VEC, NV, R>(x, nb, rows, n, bx[sl]);
+        load_stats<R>(rstd, nb, rows, brs[sl]);
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             dd[k] = 0.f;
 #pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                IO::to_float(cg[k][i], g[k][i]);
-                IO::to_float(cx[k][i], xv[k][i]);
+            for (int i = 0; i < NV; ++i)
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) dd[k] = fmaf(g[k][i][j] * wv[i][j], xv[k][i][j], dd[k]);
-            }
         }
         block_reduce_n<R, false>(dd, red, par);
 #pragma unroll
@@ -370,16 +402,7 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
                 IO::store(rx, i, g[k][i]);
             }
         }
-#pragma unroll
-        for (int k = 0; k < R; ++k) {
-#pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                cg[k][i] = ng[k][i];
-                cx[k][i] = nx[k][i];
-            }
-            crs[k] = nrs[k];
-        }
-    }
+    });
     const rsrc_t rw = make_rsrc(ws + (int64_t)blockIdx.x * n, (uint32_t)(n * 4));
 #pragma unroll
     for (int i = 0; i < NV; ++i)
@@ -392,7 +415,7 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
 // ------------------------------------------------------------------ layer norm
 // mu = mean(x); rstd = 1/sqrt(mean((x-mu)^2) + eps); y = (x-mu) rstd w + b
 // (_layer_norm!, src/layer_norm.jl:8-63).
-template <typename T, int VEC, int NV>
+template <typename T, int VEC, int NV, int D>
 __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ x, const void* __restrict__ w,
                                                            const void* __restrict__ b, int dtw, T* __restrict__ y,
                                                            float* __restrict__ mu, float* __restrict__ rstd,
@@ -409,20 +432,24 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ 
     }
     const float inv_n = 1.0f / (float)n;
     const int64_t nblk = (rows + R - 1) / R;
-    typename IO::raw cur[R][NV], nxt[R][NV];
-    load_rows<T, VEC, NV, R>(x, blockIdx.x, rows, n, cur);
-    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
-        load_rows<T, VEC, NV, R>(x, rb + gridDim.x, rows, n, nxt);
+    typename IO::raw buf[D][R][NV];
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_rows<T, VEC, NV, R>(x, blockIdx.x + (int64_t)d * gridDim.x, rows, n, buf[d]);
+    for_row_blocks<D>(nblk, [&](auto slot, int64_t rb) {
+        constexpr int sl = decltype(slot)::value;
         float v[R][NV][VEC], m[R], q[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) IO::to_float(buf[sl][k][i], v[k][i]);
+        load_rows<T, VEC, NV, R>(x, rb + (int64_t)D * gridDim.x, rows, n, buf[sl]);
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             m[k] = 0.f;
 #pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                IO::to_float(cur[k][i], v[k][i]);
+            for (int i = 0; i < NV; ++i)
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) m[k] += v[k][i][j];
-            }
         }
         block_reduce_n<R, false>(m, red, par);
 #pragma unroll
@@ -454,17 +481,13 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ 
                 IO::store(ry, i, v[k][i]);
             }
         }
-#pragma unroll
-        for (int k = 0; k < R; ++k)
-#pragma unroll
-            for (int i = 0; i < NV; ++i) cur[k][i] = nxt[k][i];
-    }
+    });
 }
 
 // Per row: xn = (x-mu) rstd; c1 = mean(w dy xn); c2 = mean(w dy);
 // dx = (w dy - (xn c1 + c2)) rstd; partials of dw = sum dy xn and db = sum dy go to
 // ws[blockIdx.x, :] and ws[grid + blockIdx.x, :] (_∇layer_norm!, src/layer_norm.jl:65-148).
-template <typename T, int VEC, int NV>
+template <typename T, int VEC, int NV, int D>
 __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ dy, const float* __restrict__ mu,
                                                            const float* __restrict__ rstd, const T* __restrict__ x,
                                                            const void* __restrict__ w, int dtw, T* __restrict__ dx,
@@ -482,33 +505,47 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
     }
     const float inv_n = 1.0f / (float)n;
     const int64_t nblk = (rows + R - 1) / R;
-    typename IO::raw cg[R][NV], cx[R][NV], ng[R][NV], nx[R][NV];
-    float cm[R], crs[R], nm[R], nrs[R];
-    load_rows<T, VEC, NV, R>(dy, blockIdx.x, rows, n, cg);
-    load_rows<T, VEC, NV, R>(x, blockIdx.x, rows, n, cx);
-    load_stats<R>(mu, blockIdx.x, rows, cm);
-    load_stats<R>(rstd, blockIdx.x, rows, crs);
-    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
-        load_rows<T, VEC, NV, R>(dy, rb + gridDim.x, rows, n, ng);
-        load_rows<T, VEC, NV, R>(x, rb + gridDim.x, rows, n, nx);
-        load_stats<R>(mu, rb + gridDim.x, rows, nm);
-        load_stats<R>(rstd, rb + gridDim.x, rows, nrs);
-        float g[R][NV][VEC], xv[R][NV][VEC], c12[2 * R];
+    typename IO::raw bg[D][R][NV], bx[D][R][NV];
+    float bm[D][R], brs[D][R];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const int64_t b0 = blockIdx.x + (int64_t)d * gridDim.x;
+        load_rows<T, VEC, NV, R>(dy, b0, rows, n, bg[d]);
+        load_rows<T, VEC, NV, R>(x, b0, rows, n, bx[d]);
+        load_stats<R>(mu, b0, rows, bm[d]);
+        load_stats<R>(rstd, b0, rows, brs[d]);
+    }
+    for_row_blocks<D>(nblk, [&](auto slot, int64_t rb) {
+        constexpr int sl = decltype(slot)::value;
+        float g[R][NV][VEC], xv[R][NV][VEC], c12[2 * R], crs[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const float cm = bm[sl][k];
+            crs[k] = brs[sl][k];
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                IO::to_float(bg[sl][k][i], g[k][i]);
+                IO::to_float(bx[sl][k][i], xv[k][i]);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) xv[k][i][j] = (xv[k][i][j] - cm) * crs[k];  // xn
+            }
+        }
+        const int64_t nb = rb + (int64_t)D * gridDim.x;
+        load_rows<T, VEC, NV, R>(dy, nb, rows, n, bg[sl]);
+        load_rows<T, VEC, NV, R>(x, nb, rows, n, bx[sl]);
+        load_stats<R>(mu, nb, rows, bm[sl]);
+        load_stats<R>(rstd, nb, rows, brs[sl]);
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             c12[2 * k] = c12[2 * k + 1] = 0.f;
 #pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                IO::to_float(cg[k][i], g[k][i]);
-                IO::to_float(cx[k][i], xv[k][i]);
+            for (int i = 0; i < NV; ++i)
 #pragma unroll
-                for (int j = 0; j < VEC; ++j) {
-                    xv[k][i][j] = (xv[k][i][j] - cm[k]) * crs[k];  // xn (zero-padded slots give g = 0)
+                for (int j = 0; j < VEC; ++j) {  // zero-padded slots give g = 0
                     const float wdy = wv[i][j] * g[k][i][j];
                     c12[2 * k] = fmaf(wdy, xv[k][i][j], c12[2 * k]);
                     c12[2 * k + 1] += wdy;
                 }
-            }
         }
         block_reduce_n<2 * R, false>(c12, red, par);
 #pragma unroll
@@ -527,17 +564,7 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
                 IO::store(rx, i, o);
             }
         }
-#pragma unroll
-        for (int k = 0; k < R; ++k) {
-#pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                cg[k][i] = ng[k][i];
-                cx[k][i] = nx[k][i];
-            }
-            cm[k] = nm[k];
-            crs[k] = nrs[k];
-        }
-    }
+    });
     const rsrc_t rw = make_rsrc(ws + (int64_t)blockIdx.x * n, (uint32_t)(n * 4));
     const rsrc_t rb = make_rsrc(ws + ((int64_t)gridDim.x + blockIdx.x) * n, (uint32_t)(n * 4));
 #pragma unroll
@@ -608,6 +635,11 @@ __global__ __launch_bounds__(256) void colsum_stage2_kernel(const float* __restr
 }
 
 // ------------------------------------------------------------------ dispatch
+
+// Row blocks in flight ahead of the one being computed by the norm backward: two while
+// a register slot (dy and x of R rows) is at most 4 vectors per tensor per thread.  The
+// forward kernels keep one: a second measured slower there.
+template <int NV> struct BwdDepth { static constexpr int D = RowsPerIter<NV>::R * NV <= 4 ? 2 : 1; };
 
 static int num_cus() {
     static int cus = 0;
@@ -700,7 +732,7 @@ template <typename T, int VEC, int NV>
 struct RmsFwd {
     static bool run(hipStream_t s, const void* x, const void* w, int dtw, void* y, float* rstd, int64_t n,
                     int64_t rows, float eps, float offset) {
-        const auto k = rms_fwd_kernel<T, VEC, NV>;
+        const auto k = rms_fwd_kernel<T, VEC, NV, 1>;
         static const int fit = fit_per_cu(k);
         k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 1)), dim3(kThreads), 0, s>>>(
             (const T*)x, w, dtw, (T*)y, rstd, n, rows, eps, offset);
@@ -711,7 +743,7 @@ template <typename T, int VEC, int NV>
 struct RmsBwd {
     static bool run(hipStream_t s, const void* dy, const float* rstd, const void* x, const void* w, int dtw,
                     float offset, void* dx, float* ws, int64_t groups, int64_t n, int64_t rows) {
-        rms_bwd_kernel<T, VEC, NV><<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>(
+        rms_bwd_kernel<T, VEC, NV, BwdDepth<NV>::D><<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>(
             (const T*)dy, rstd, (const T*)x, w, dtw, offset, (T*)dx, ws, n, rows);
         return true;
     }
@@ -720,7 +752,7 @@ template <typename T, int VEC, int NV>
 struct LnFwd {
     static bool run(hipStream_t s, const void* x, const void* w, const void* b, int dtw, void* y, float* mu,
                     float* rstd, int64_t n, int64_t rows, float eps) {
-        const auto k = ln_fwd_kernel<T, VEC, NV>;
+        const auto k = ln_fwd_kernel<T, VEC, NV, 1>;
         static const int fit = fit_per_cu(k);
         k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 1)), dim3(kThreads), 0, s>>>(
             (const T*)x, w, b, dtw, (T*)y, mu, rstd, n, rows, eps);
@@ -731,7 +763,7 @@ template <typename T, int VEC, int NV>
 struct LnBwd {
     static bool run(hipStream_t s, const void* dy, const float* mu, const float* rstd, const void* x,
                     const void* w, int dtw, void* dx, float* ws, int64_t groups, int64_t n, int64_t rows) {
-        ln_bwd_kernel<T, VEC, NV><<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>(
+        ln_bwd_kernel<T, VEC, NV, BwdDepth<NV>::D><<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>(
             (const T*)dy, mu, rstd, (const T*)x, w, dtw, (T*)dx, ws, n, rows);
         return true;
     }
