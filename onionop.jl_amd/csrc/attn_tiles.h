@@ -122,6 +122,39 @@ struct TileDMA {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, base, 16, (int)off, 0, 0, 0);
         }
     }
+
+    // The same loads with the per-lane byte offsets (relative to the tile's first row)
+    // computed once, outside the tile loop: a tile then costs only scalar work to build a
+    // resource that starts at its first row and ends at the slice's end, so rows past the
+    // slice still read zeros, and no vector instructions go to address arithmetic.
+    struct Offs { uint32_t o[NI]; };
+    __device__ __forceinline__ static Offs offsets(int t, int wave) {
+        Offs r;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int slot = i * NT + wave * 64 + (t & 63);
+            const int row = slot / SPR, ch = slot - row * SPR;
+            r.o[i] = ch < CPR ? (uint32_t)row * (uint32_t)(E * 2) + (uint32_t)ch * 16u : 0xFFFFFFF0u;
+        }
+        return r;
+    }
+    // Rows [r0, r0 + NR) of the slice of `nrows` rows at `slice` into the LDS tile at dst.
+    __device__ __forceinline__ static void load(const T* slice, int nrows, int r0, const Offs& off, T* dst, int t,
+                                                int wave) {
+        typedef __attribute__((address_space(3))) void lds_void;
+        const rsrc_t rs = make_rsrc(slice + (int64_t)r0 * E, nrows > r0 ? (uint32_t)(nrows - r0) * (uint32_t)(E * 2) : 0u);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int slot0 = i * NT + wave * 64;
+            if constexpr (NS % NT != 0) {
+                if (slot0 >= NS) continue;
+            }
+            if constexpr (NS % 64 != 0) {
+                if (slot0 + (t & 63) >= NS) continue;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + slot0 * 8), 16, (int)off.o[i], 0, 0, 0);
+        }
+    }
 };
 
 // Zero columns [E, DS) of two NR-row LDS tiles (the padding read as rows E..31 of a 32-row
