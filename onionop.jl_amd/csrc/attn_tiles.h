@@ -96,7 +96,7 @@ struct TileRegs {
 // publishes the tile.
 template <typename T, int NR, int E, int NT>
 struct TileDMA {
-    static_assert(sizeof(T) == 2 && TileCfg<T, E>::DS == E + 8, "16-bit tiles with one padding chunk per row");
+    static constexpr bool kOK = sizeof(T) == 2 && TileCfg<T, E>::DS == E + 8;  // one padding chunk per row
     static constexpr int CPR = E * 2 / 16;  // data chunks per row
     static constexpr int SPR = CPR + 1;     // LDS slots per row
     static constexpr int NS = NR * SPR;     // slots per tile
@@ -105,6 +105,7 @@ struct TileDMA {
     // Rows [r0, r0 + NR) of the slice behind `rs` into the LDS tile at dst; t is the
     // thread's index among the NT threads that share the tile, wave = t / 64 (uniform).
     __device__ __forceinline__ static void load(rsrc_t rs, int r0, T* dst, int t, int wave) {
+        static_assert(kOK, "16-bit tiles with one padding chunk per row");
         typedef __attribute__((address_space(3))) void lds_void;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -141,6 +142,7 @@ struct TileDMA {
     // Rows [r0, r0 + NR) of the slice of `nrows` rows at `slice` into the LDS tile at dst.
     __device__ __forceinline__ static void load(const T* slice, int nrows, int r0, const Offs& off, T* dst, int t,
                                                 int wave) {
+        static_assert(kOK, "16-bit tiles with one padding chunk per row");
         typedef __attribute__((address_space(3))) void lds_void;
         const rsrc_t rs = make_rsrc(slice + (int64_t)r0 * E, nrows > r0 ? (uint32_t)(nrows - r0) * (uint32_t)(E * 2) : 0u);
 #pragma unroll
