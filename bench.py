@@ -165,8 +165,10 @@ def memory_bound(torch, nnop, dev, reps=10):
         return [make() for _ in range(n_sets)]
 
     def measure(name, sets, call, nbytes):
-        for s in sets:  # warm
-            call(s)
+        for _ in range(2):  # warm (the first launches of a kernel run slower)
+            for s in sets:
+                call(s)
+        torch.cuda.synchronize()
         i = [0]
 
         def one():
