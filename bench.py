@@ -151,7 +151,7 @@ def measured_traffic(kernel):
     return None if rec is None else int(rec["bytes"])
 
 
-def memory_bound(torch, nnop, dev, reps=10):
+def memory_bound(torch, nnop, dev, reps=30):
     """GB/s of the HBM-bound kernels over buffer sets rotated past the 256 MB MALL."""
     from nnop import _lib
     from nnop._util import ptr
@@ -165,7 +165,7 @@ def memory_bound(torch, nnop, dev, reps=10):
         return [make() for _ in range(n_sets)]
 
     def measure(name, sets, call, nbytes):
-        for _ in range(2):  # warm (the first launches of a kernel run slower)
+        for _ in range(5):  # warm (the first launches of a kernel run slower)
             for s in sets:
                 call(s)
         torch.cuda.synchronize()
@@ -267,8 +267,10 @@ def cpu_baseline(E=64, L=4096, H=4, B=4, threads=None):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    # The GPU reaches its steady clocks only after some 30 ms of this load (the first 50
+    # steps average ~1.8x the steady step time), so the default warmup is 200 steps (~40 ms).
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-memory", action="store_true", help="skip the HBM-bound kernel set")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
