@@ -191,6 +191,12 @@ def memory_bound(torch, nnop, dev, reps=30):
             lambda s: _lib.check(L.onionop_softmax_bwd(stream, 0, N, M, ptr(s[0]), ptr(s[1]), ptr(s[2]))),
             3 * M * N * 4)
     del sets
+    # second-order pullback: reads g, dy, y; writes d_dy, d_y
+    sets = rot(6, lambda: tuple(torch.randn((M, N), generator=g).to(dev) for _ in range(5)))
+    measure("softmax_bwd_bwd_f32_8192x1024", sets,
+            lambda s: _lib.check(L.onionop_softmax_bwd_bwd(stream, 0, N, M, ptr(s[0]), ptr(s[1]), ptr(s[2]),
+                                                           ptr(s[3]), ptr(s[4]))), 5 * M * N * 4)
+    del sets
 
     # rms / layer norm bf16, Julia x (4096, 16384) -> torch (16384, 4096)
     emb, n = 4096, 16384

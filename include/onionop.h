@@ -52,7 +52,7 @@ const char* onionop_last_error(void);
 
 /* ABI revision of this header (bumped on any signature change). */
 int onionop_abi_version(void);
-#define ONIONOP_ABI_VERSION 1
+#define ONIONOP_ABI_VERSION 2
 
 /* LDS bytes per workgroup of `device` (cached once per device).
  * Replaces NNop.shared_memory / _shared_memory(::ROCBackend)
@@ -154,6 +154,18 @@ int onionop_softmax_fwd(void* stream, int dtype, int64_t N, int64_t M,
  */
 int onionop_softmax_bwd(void* stream, int dtype, int64_t N, int64_t M,
                         const void* dy, const void* y, void* dx);
+
+/*
+ * Pullback of the softmax backward, for second derivatives: given g = dL/d(dx) of
+ * dx = onionop_softmax_bwd(dy, y), with s = sum(dy .* y) and u = sum(g .* y) per column,
+ *   d_dy = y .* (g - u),   d_y = g .* (dy - s) - dy .* u.
+ * Replaces the reference's second-order path, the `within_gradient` branch of
+ * `∇online_softmax` (src/softmax.jl:71-74), which keeps the backward as differentiable
+ * broadcasts for the AD system.  All five tensors share `dtype`.
+ */
+int onionop_softmax_bwd_bwd(void* stream, int dtype, int64_t N, int64_t M,
+                            const void* g, const void* dy, const void* y,
+                            void* d_dy, void* d_y);
 
 /* ------------------------------------------------------------------- RMS norm */
 

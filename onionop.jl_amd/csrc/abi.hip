@@ -237,6 +237,19 @@ int onionop_softmax_bwd(void* stream, int dtype, int64_t N, int64_t M, const voi
     return check_launch("∇online_softmax");
 }
 
+int onionop_softmax_bwd_bwd(void* stream, int dtype, int64_t N, int64_t M, const void* g, const void* dy,
+                            const void* y, void* d_dy, void* d_y) {
+    const char* what = "∇online_softmax pullback";
+    int st = check_rows(what, dtype, N, M);
+    if (st) return st;
+    if (N * M > 0 && (!g || !dy || !y || !d_dy || !d_y)) return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);
+    if (!aligned16(g) || !aligned16(dy) || !aligned16(y) || !aligned16(d_dy) || !aligned16(d_y))
+        return fail(ONIONOP_E_SHAPE, "%s: tensors must be 16-byte aligned", what);
+    if (!onionop::launch_softmax_bwd_bwd((hipStream_t)stream, dtype, N, M, g, dy, y, d_dy, d_y))
+        return fail(ONIONOP_E_UNSUPPORTED, "%s: no kernel for N=%lld", what, (long long)N);
+    return check_launch(what);
+}
+
 // ------------------------------------------------------------------- RMS norm
 
 int onionop_rms_norm_fwd(void* stream, int dtype_x, int dtype_w, int64_t emb, int64_t n, const void* x,

@@ -32,6 +32,8 @@ bool launch_attn_bwd(hipStream_t s, int dt, const AttnArgs& a, int stages);
 
 bool launch_softmax_fwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* x, void* y);
 bool launch_softmax_bwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* dy, const void* y, void* dx);
+bool launch_softmax_bwd_bwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* g, const void* dy,
+                            const void* y, void* d_dy, void* d_y);
 bool launch_rms_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* x, const void* w,
                     float eps, float offset, void* y, float* rstd);
 bool launch_rms_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* dy, const float* rstd,

@@ -266,6 +266,71 @@ __global__ __launch_bounds__(kThreads) void softmax_bwd_kernel(const T* __restri
     }
 }
 
+// Pullback of the softmax backward (second order; src/softmax.jl:70-80, the
+// within_gradient branch at :71-74): for dx = y (dy - s), s = sum(dy y), and upstream
+// G = dL/d(dx), with u = sum(G y):  d_dy = y (G - u),  d_y = G (dy - s) - dy u.
+template <typename T, int VEC, int NV>
+__global__ __launch_bounds__(kThreads) void softmax_bwd2_kernel(const T* __restrict__ g, const T* __restrict__ dy,
+                                                                 const T* __restrict__ y, T* __restrict__ d_dy,
+                                                                 T* __restrict__ d_y, int64_t n, int64_t rows) {
+    typedef RowIO<T, VEC> IO;
+    constexpr int R = RowsPerIter<NV>::R;
+    __shared__ float red[2 * kWaves * 2 * R];
+    int par = 0;
+    const int64_t nblk = (rows + R - 1) / R;
+    typename IO::raw cg[R][NV], cd[R][NV], cy[R][NV], ng[R][NV], nd[R][NV], ny[R][NV];
+    load_rows<T, VEC, NV, R>(g, blockIdx.x, rows, n, cg);
+    load_rows<T, VEC, NV, R>(dy, blockIdx.x, rows, n, cd);
+    load_rows<T, VEC, NV, R>(y, blockIdx.x, rows, n, cy);
+    for (int64_t rb = blockIdx.x; rb < nblk; rb += gridDim.x) {
+        load_rows<T, VEC, NV, R>(g, rb + gridDim.x, rows, n, ng);
+        load_rows<T, VEC, NV, R>(dy, rb + gridDim.x, rows, n, nd);
+        load_rows<T, VEC, NV, R>(y, rb + gridDim.x, rows, n, ny);
+        float gv[R][NV][VEC], dv[R][NV][VEC], yv[R][NV][VEC], su[2 * R];
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            su[2 * k] = su[2 * k + 1] = 0.f;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                IO::to_float(cg[k][i], gv[k][i]);
+                IO::to_float(cd[k][i], dv[k][i]);
+                IO::to_float(cy[k][i], yv[k][i]);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {  // elements past n read 0 and add nothing
+                    su[2 * k] = fmaf(dv[k][i][j], yv[k][i][j], su[2 * k]);
+                    su[2 * k + 1] = fmaf(gv[k][i][j], yv[k][i][j], su[2 * k + 1]);
+                }
+            }
+        }
+        block_reduce_n<2 * R, false>(su, red, par);
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const float sk = su[2 * k], uk = su[2 * k + 1];
+            const rsrc_t ra = row_rsrc(d_dy, rb * R + k, rows, n);
+            const rsrc_t rc = row_rsrc(d_y, rb * R + k, rows, n);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                float a[VEC], c[VEC];
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    a[j] = yv[k][i][j] * (gv[k][i][j] - uk);
+                    c[j] = gv[k][i][j] * (dv[k][i][j] - sk) - dv[k][i][j] * uk;
+                }
+                IO::store(ra, i, a);
+                IO::store(rc, i, c);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                cg[k][i] = ng[k][i];
+                cd[k][i] = nd[k][i];
+                cy[k][i] = ny[k][i];
+            }
+    }
+}
+
 // ------------------------------------------------------------------ RMS norm
 // rstd = 1/sqrt(mean(x^2) + eps); y = (offset + w) x rstd (_rms_norm!, src/rms_norm.jl:3-38).
 template <typename T, int VEC, int NV, int D>
@@ -729,6 +794,17 @@ struct SoftmaxBwd {
     }
 };
 template <typename T, int VEC, int NV>
+struct SoftmaxBwd2 {
+    static bool run(hipStream_t s, const void* g, const void* dy, const void* y, void* d_dy, void* d_y, int64_t n,
+                    int64_t rows) {
+        const auto k = softmax_bwd2_kernel<T, VEC, NV>;
+        static const int fit = fit_per_cu(k);
+        k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 3)), dim3(kThreads), 0, s>>>(
+            (const T*)g, (const T*)dy, (const T*)y, (T*)d_dy, (T*)d_y, n, rows);
+        return true;
+    }
+};
+template <typename T, int VEC, int NV>
 struct RmsFwd {
     static bool run(hipStream_t s, const void* x, const void* w, int dtw, void* y, float* rstd, int64_t n,
                     int64_t rows, float eps, float offset) {
@@ -821,6 +897,12 @@ bool launch_softmax_fwd(hipStream_t s, int dt, int64_t n, int64_t rows, const vo
 bool launch_softmax_bwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* dy, const void* y, void* dx) {
     if (rows == 0 || n == 0) return true;
     ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, SoftmaxBwd>(n, s, dy, y, dx, n, rows));
+    return true;
+}
+bool launch_softmax_bwd_bwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* g, const void* dy,
+                            const void* y, void* d_dy, void* d_y) {
+    if (rows == 0 || n == 0) return true;
+    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, SoftmaxBwd2>(n, s, g, dy, y, d_dy, d_y, n, rows));
     return true;
 }
 bool launch_rms_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* x, const void* w,

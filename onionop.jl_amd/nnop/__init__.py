@@ -12,6 +12,7 @@ Reference names -> here:
   NNop.flash_attention / _flash_attention / ∇flash_attention
       -> flash_attention / _flash_attention / grad_flash_attention
   NNop.online_softmax / ∇online_softmax -> online_softmax / grad_online_softmax
+  (second order, the within_gradient branch of ∇online_softmax) -> grad_online_softmax_pullback
   NNop.rms_norm / _rms_norm / ∇rms_norm -> rms_norm / _rms_norm / grad_rms_norm
   NNop.layer_norm / _layer_norm / ∇layer_norm -> layer_norm / _layer_norm / grad_layer_norm
   NNop.llama_rope / _llama_rope / ∇llama_rope / LlamaRotaryEmbedding -> same names
@@ -20,12 +21,12 @@ from ._lib import LIB_PATH, NNopError, lib
 from .attention import _flash_attention, attention_scale, flash_attention, grad_flash_attention
 from .norms import _layer_norm, _rms_norm, grad_layer_norm, grad_rms_norm, layer_norm, rms_norm
 from .rope import LlamaRotaryEmbedding, _llama_rope, grad_llama_rope, llama_rope
-from .softmax import _online_softmax, grad_online_softmax, online_softmax
+from .softmax import _online_softmax, grad_online_softmax, grad_online_softmax_pullback, online_softmax
 
 __all__ = [
     "LIB_PATH", "NNopError", "lib",
     "flash_attention", "_flash_attention", "grad_flash_attention", "attention_scale",
-    "online_softmax", "_online_softmax", "grad_online_softmax",
+    "online_softmax", "_online_softmax", "grad_online_softmax", "grad_online_softmax_pullback",
     "rms_norm", "_rms_norm", "grad_rms_norm",
     "layer_norm", "_layer_norm", "grad_layer_norm",
     "llama_rope", "_llama_rope", "grad_llama_rope", "LlamaRotaryEmbedding",

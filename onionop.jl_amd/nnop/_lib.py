@@ -37,6 +37,7 @@ SIGNATURES = {
                                        _vp, _i, _f, _i, _vp, _vp, _vp, _sz]),
     "onionop_softmax_fwd": (_i, [_vp, _i, _i64, _i64, _vp, _vp]),
     "onionop_softmax_bwd": (_i, [_vp, _i, _i64, _i64, _vp, _vp, _vp]),
+    "onionop_softmax_bwd_bwd": (_i, [_vp, _i, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "onionop_rms_norm_fwd": (_i, [_vp, _i, _i, _i64, _i64, _vp, _vp, _f, _f, _vp, _vp]),
     "onionop_rms_norm_bwd_workspace": (_sz, [_i64, _i64]),
     "onionop_rms_norm_bwd": (_i, [_vp, _i, _i, _i64, _i64, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _sz]),
@@ -46,7 +47,7 @@ SIGNATURES = {
     "onionop_llama_rope": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _f, _vp, _vp]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class NNopError(RuntimeError):

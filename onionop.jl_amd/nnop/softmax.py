@@ -40,8 +40,39 @@ def grad_online_softmax(dy, y):
     return dx
 
 
+def grad_online_softmax_pullback(g, dy, y):
+    """Pullback of ∇online_softmax for second derivatives (the reference keeps them through
+    its within_gradient branch, src/softmax.jl:71-74): for g = dL/d(dx),
+    returns (d_dy, d_y) = (y (g - u), g (dy - s) - dy u), s = sum(dy y), u = sum(g y)."""
+    y = device_tensor(y, "∇online_softmax pullback")
+    dy = device_tensor(dy, "∇online_softmax pullback").to(y.dtype)
+    g = device_tensor(g, "∇online_softmax pullback").to(y.dtype)
+    if dy.shape != y.shape or g.shape != y.shape:
+        raise ValueError("g and Δ must have the shape of y")
+    dt = dtype_code(y, "∇online_softmax pullback")
+    M, N = _as_matrix(y).shape
+    d_dy, d_y = torch.empty_like(y), torch.empty_like(y)
+    _lib.check(_lib.lib().onionop_softmax_bwd_bwd(stream_of(y), dt, N, M, ptr(g), ptr(dy), ptr(y), ptr(d_dy),
+                                                  ptr(d_y)))
+    return d_dy, d_y
+
+
+class _GradOnlineSoftmaxFn(torch.autograd.Function):
+    """∇online_softmax as a differentiable operation (its own pullback on the GPU)."""
+
+    @staticmethod
+    def forward(ctx, dy, y):
+        ctx.save_for_backward(dy, y)
+        return grad_online_softmax(dy, y)
+
+    @staticmethod
+    def backward(ctx, g):
+        dy, y = ctx.saved_tensors
+        return grad_online_softmax_pullback(g.contiguous(), dy, y)
+
+
 class _OnlineSoftmaxFn(torch.autograd.Function):
-    """rrule(online_softmax) (src/softmax.jl:82-86)."""
+    """rrule(online_softmax) (src/softmax.jl:82-86); its backward is itself differentiable."""
 
     @staticmethod
     def forward(ctx, x):
@@ -52,7 +83,7 @@ class _OnlineSoftmaxFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         (y,) = ctx.saved_tensors
-        return grad_online_softmax(dy.contiguous(), y)
+        return _GradOnlineSoftmaxFn.apply(dy.contiguous(), y)
 
 
 def online_softmax(x):

@@ -62,6 +62,7 @@ def lib():
         L.orc_round_array.argtypes = [ctypes.c_int, _i64, _dp, _dp]
         L.orc_softmax_fwd.argtypes = [ctypes.c_int, _i64, _i64, _dp, _dp]
         L.orc_softmax_bwd.argtypes = [ctypes.c_int, _i64, _i64, _dp, _dp, _dp]
+        L.orc_softmax_bwd_bwd.argtypes = [_i64, _i64, _dp, _dp, _dp, _dp, _dp]
         L.orc_rms_fwd.argtypes = [ctypes.c_int, _i64, _i64, _dp, _dp, ctypes.c_double,
                                   ctypes.c_double, _dp, _dp]
         L.orc_rms_bwd.argtypes = [ctypes.c_int, _i64, _i64, _dp, _dp, _dp, _dp,
@@ -128,6 +129,17 @@ def softmax_bwd(dy, y, mode=EXACT):
     dx = np.empty_like(y)
     lib().orc_softmax_bwd(mode, N, M, pdy, py, _ptr(dx))
     return dx
+
+
+def softmax_bwd_bwd(g, dy, y):
+    """Pullback of softmax_bwd(dy, y) for upstream gradient g: (d_dy, d_y), float64."""
+    g, pg = _d(g)
+    dy, pdy = _d(dy)
+    y, py = _d(y)
+    M, N = (1, y.shape[0]) if y.ndim == 1 else y.shape
+    d_dy, d_y = np.empty_like(y), np.empty_like(y)
+    lib().orc_softmax_bwd_bwd(N, M, pg, pdy, py, _ptr(d_dy), _ptr(d_y))
+    return d_dy, d_y
 
 
 # ------------------------------------------------------------------ norms

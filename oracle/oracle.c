@@ -119,6 +119,29 @@ void orc_softmax_fwd(int mode, i64 N, i64 M, const double* x, double* y) {
     }
 }
 
+/* Pullback of dx = dy .* y - y .* s, s = sum(dy .* y; dims=1) (src/softmax.jl:70-80; the
+ * within_gradient branch at :71-74 keeps this second derivative available): for
+ * G = dL/d(dx), with u = sum(G .* y; dims=1),
+ *   dL/d(dy) = y .* (G - u),   dL/d(y) = G .* (dy - s) - dy .* u.     Float64. */
+void orc_softmax_bwd_bwd(i64 N, i64 M, const double* G, const double* dy, const double* y, double* d_dy,
+                         double* d_y) {
+#pragma omp parallel for schedule(static)
+    for (i64 j = 0; j < M; ++j) {
+        const double* gc = G + j * N;
+        const double* dc = dy + j * N;
+        const double* yc = y + j * N;
+        double s = 0.0, u = 0.0;
+        for (i64 i = 0; i < N; ++i) {
+            s += dc[i] * yc[i];
+            u += gc[i] * yc[i];
+        }
+        for (i64 i = 0; i < N; ++i) {
+            d_dy[j * N + i] = yc[i] * (gc[i] - u);
+            d_y[j * N + i] = gc[i] * (dc[i] - s) - dc[i] * u;
+        }
+    }
+}
+
 /* dx = dy .* y - y .* sum(dy .* y; dims=1)  (src/softmax.jl:70-80). */
 void orc_softmax_bwd(int mode, i64 N, i64 M, const double* dy, const double* y, double* dx) {
 #pragma omp parallel for schedule(static)

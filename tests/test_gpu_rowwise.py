@@ -51,6 +51,41 @@ def test_softmax_autograd(dev):
     check({"dx": rel_err(host(x.grad), oracle.softmax_bwd(g, oracle.softmax_fwd(xn)))}, 1e-5)
 
 
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("n", [33, 256, 513, 4095, 8192])
+def test_softmax_bwd_bwd(dev, dt, n):
+    """Pullback of the softmax backward (second order) against the oracle's float64 form."""
+    dtype = DTYPES[dt]
+    rng = np.random.default_rng(100 + n)
+    x, _ = make(rng, (3, n), dtype, dev, kind="uniform")
+    y = nnop._online_softmax(x)
+    dy, dyn = make(rng, (3, n), dtype, dev)
+    g, gn = make(rng, (3, n), dtype, dev)
+    d_dy, d_y = nnop.grad_online_softmax_pullback(g, dy, y)
+    torch.cuda.synchronize()
+    r_dy, r_y = oracle.softmax_bwd_bwd(gn, dyn, host(y))
+    check({"d_dy": rel_err(host(d_dy), r_dy), "d_y": rel_err(host(d_y), r_y)},
+          TOL[dtype] if dtype != torch.float32 else 1e-5)
+
+
+def test_softmax_second_order_autograd(dev):
+    """d/dx <G, d<dy, softmax(x)>/dx> through two GPU backward launches (create_graph)."""
+    rng = np.random.default_rng(7)
+    x, xn = make(rng, (4, 200), torch.float32, dev)
+    dy, dyn = make(rng, (4, 200), torch.float32, dev)
+    G, Gn = make(rng, (4, 200), torch.float32, dev)
+    x.requires_grad_(True)
+    dy.requires_grad_(True)
+    y = nnop.online_softmax(x)
+    (gx,) = torch.autograd.grad(y, x, dy, create_graph=True)
+    gdy, gx2 = torch.autograd.grad(gx, (dy, x), G)
+    torch.cuda.synchronize()
+    y_r = oracle.softmax_fwd(xn)
+    r_dy, r_y = oracle.softmax_bwd_bwd(Gn, dyn, y_r)
+    check({"gx": rel_err(host(gx), oracle.softmax_bwd(dyn, y_r)), "d_dy": rel_err(host(gdy), r_dy),
+           "d_x": rel_err(host(gx2), oracle.softmax_bwd(r_y, y_r))}, 1e-5)
+
+
 # ------------------------------------------------------------------ RMS norm
 
 RMS_CASES = [(emb, n, off) for emb in (15, 255, 256, 257, 511, 512, 513, 1024)

@@ -82,6 +82,36 @@ def test_softmax_bwd():
     assert np.allclose(dx[sel], fd[sel], atol=1e-8)
 
 
+def test_softmax_bwd_bwd():
+    """Pullback of the softmax backward (second order): finite differences of
+    <G, softmax_bwd(dy, y)> in dy and in y, and torch float64 double backward."""
+    rng = RNG(31)
+    x = rng.standard_normal((4, 48))
+    dy = rng.standard_normal((4, 48))
+    G = rng.standard_normal((4, 48))
+    y = oracle.softmax_fwd(x)
+    d_dy, d_y = oracle.softmax_bwd_bwd(G, dy, y)
+    h = 1e-6
+    for j in range(4):
+        for i in range(0, 48, 5):
+            for arg, got in ((0, d_dy), (1, d_y)):
+                a = [dy.copy(), y.copy()]
+                b = [dy.copy(), y.copy()]
+                a[arg][j, i] += h
+                b[arg][j, i] -= h
+                fd = (np.sum(G * oracle.softmax_bwd(*a)) - np.sum(G * oracle.softmax_bwd(*b))) / (2 * h)
+                assert abs(got[j, i] - fd) < 1e-7, (arg, j, i, got[j, i], fd)
+    # library routine: torch autograd of its own float64 softmax backward
+    xt = torch.from_numpy(x).requires_grad_(True)
+    dyt = torch.from_numpy(dy).requires_grad_(True)
+    yt = torch.softmax(xt, -1)
+    (gx,) = torch.autograd.grad(yt, xt, dyt, create_graph=True)
+    gdy, gx2 = torch.autograd.grad(gx, (dyt, xt), torch.from_numpy(G))
+    assert rel_err(d_dy, gdy.numpy()) < 1e-13
+    # through y = softmax(x): dL/dx = softmax_bwd(d_y, y)
+    assert rel_err(oracle.softmax_bwd(d_y, y), gx2.numpy()) < 1e-12
+
+
 # ------------------------------------------------------------------ RMS norm
 
 @pytest.mark.parametrize("offset", [0.0, 1.0])
