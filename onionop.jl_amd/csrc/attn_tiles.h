@@ -9,10 +9,14 @@
 namespace onionop {
 
 // LDS row stride (elements) of a natural (rows x EO) tile.  16-bit: 16 bytes of padding,
-// keeping rows 16-byte aligned for ds_read_b128 / b128 stores.  float32: one element,
-// making the column reads of the float32 MFMA operands conflict-free.
-template <typename T, int EO> struct TileCfg { static constexpr int DS = EO + 8; };
-template <int EO> struct TileCfg<float, EO> { static constexpr int DS = EO + 1; };
+// keeping rows 16-byte aligned for ds_read_b128 / b128 stores; WIDE: 32 bytes, with which
+// the transposed reads (ds_read_b64_tr_b16: each 16-lane group reads 4 rows x 32 bytes)
+// hit every LDS bank exactly twice, the minimum for 512 bytes over 64 four-byte banks,
+// while 16 bytes of padding give 3 (E = 32, 64) or 4 (E = 128) reads on the busiest bank.
+// float32: one element, making the column reads of the float32 MFMA operands
+// conflict-free.
+template <typename T, int EO, bool WIDE = false> struct TileCfg { static constexpr int DS = EO + (WIDE ? 16 : 8); };
+template <int EO, bool WIDE> struct TileCfg<float, EO, WIDE> { static constexpr int DS = EO + 1; };
 
 // Waits until every outstanding vector-memory load has returned (s_waitcnt vmcnt(0)).
 // Issued once after the loads that precede a software-pipelined loop, so the compiler's
@@ -89,16 +93,17 @@ struct TileRegs {
 // Direct global -> LDS staging of a 16-bit tile (buffer_load_dwordx4 ... lds): each
 // lane's 16 bytes land at the wave's LDS base + 16 * lane, so one instruction fills 64
 // consecutive 16-byte slots and no registers hold the tile in transit.  The padded layout
-// is kept (row stride DS = E + 8 elements = CPR + 1 slots): a lane whose slot is a row's
+// is kept (row stride DS elements = SPR 16-byte slots, CPR of them data): a lane whose slot is a row's
 // padding chunk, or whose row is past the slice, uses an offset past the resource's end
 // and so writes zeros without touching memory.  Completion is tracked by the vector-
 // memory counter: the waiting wave issues s_waitcnt vmcnt before the barrier that
 // publishes the tile.
-template <typename T, int NR, int E, int NT>
+template <typename T, int NR, int E, int NT, int DS = TileCfg<T, E>::DS>
 struct TileDMA {
-    static constexpr bool kOK = sizeof(T) == 2 && TileCfg<T, E>::DS == E + 8;  // one padding chunk per row
+    // 16-bit rows of E elements at an LDS row stride of DS elements (padding chunks >= 1)
+    static constexpr bool kOK = sizeof(T) == 2 && DS > E && (DS - E) % 8 == 0;
     static constexpr int CPR = E * 2 / 16;  // data chunks per row
-    static constexpr int SPR = CPR + 1;     // LDS slots per row
+    static constexpr int SPR = DS * 2 / 16; // LDS slots per row (data + padding)
     static constexpr int NS = NR * SPR;     // slots per tile
     static constexpr int NI = (NS + NT - 1) / NT;
 
