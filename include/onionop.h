@@ -137,6 +137,46 @@ int onionop_flash_attn_bwd_dq(void* stream, int dtype,
                               const void* pair, const uint8_t* kpad, int causal, float scale, int qk_fp16,
                               void* dq, void* dpair, void* workspace, size_t workspace_bytes);
 
+/* ------------------------------------------- attention, packed variable-length sequences */
+
+/*
+ * Flash attention over B packed sequences of different lengths, with no padding
+ * anywhere.  The reference expresses variable lengths only through `kpad_mask`
+ * (src/attention.jl:16,83-89), which still computes every padded query row and reads
+ * every padded key; here sequence b is rows cu_seqlens_q[b] .. cu_seqlens_q[b+1] of
+ * q (E, Tq, QH) (row-major (QH, Tq, E)) and rows cu_seqlens_k[b] .. cu_seqlens_k[b+1]
+ * of k, v (E, Tk, KH), and only those rows are read or computed.  Causal masking is
+ * within each sequence, aligned at its first row (key j <= query i).
+ *   cu_seqlens_q, cu_seqlens_k: B + 1 nondecreasing int32 device offsets, [0] = 0,
+ *     [B] <= Tq (Tk).  max_seqlen_q / max_seqlen_k bound every length (host values:
+ *     they size the launch; longer sequences are cut to them).  Offsets outside
+ *     [0, Tq] ([0, Tk]) are clamped into it.
+ *   o like q; ms, ls (Tq, QH) (row-major (QH, Tq)).  Rows not in any sequence are not
+ *     written.  No pair bias or key mask (use the dense entry points for those).
+ */
+int onionop_flash_attn_varlen_fwd(void* stream, int dtype,
+                                  int64_t E, int64_t Tq, int64_t Tk, int64_t QH, int64_t KH, int64_t B,
+                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                  const void* q, const void* k, const void* v, int causal, float scale,
+                                  void* o, float* ms, float* ls);
+
+/* Bytes of workspace onionop_flash_attn_varlen_bwd needs. */
+size_t onionop_flash_attn_varlen_bwd_workspace(int dtype, int64_t E, int64_t Tq, int64_t QH);
+
+/*
+ * Backward of onionop_flash_attn_varlen_fwd: dq, dk, dv in the packed layouts of q, k,
+ * v (dk / dv rows of keys in no sequence are not written).  Same conventions as
+ * onionop_flash_attn_bwd otherwise (qk_fp16 for Float32).
+ */
+int onionop_flash_attn_varlen_bwd(void* stream, int dtype,
+                                  int64_t E, int64_t Tq, int64_t Tk, int64_t QH, int64_t KH, int64_t B,
+                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                  const void* dO, const void* o, const float* ms, const float* ls,
+                                  const void* q, const void* k, const void* v, int causal, float scale, int qk_fp16,
+                                  void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes);
+
 /* -------------------------------------------------------------------- softmax */
 
 /*

@@ -203,6 +203,88 @@ int onionop_flash_attn_bwd_dq(void* stream, int dtype, int64_t E, int64_t QL, in
                            dpair, workspace, workspace_bytes);
 }
 
+// ------------------------------------------------------ attention, packed variable length
+
+// Extra checks of the packed entry points: per-sequence limits as in check_attn (with the
+// longest lengths), offsets present, packed lengths within the 32-bit offsets.
+static int check_varlen(const char* what, int dtype, int64_t E, int64_t Tq, int64_t Tk, int64_t QH, int64_t KH,
+                        int64_t B, const int32_t* cu_q, const int32_t* cu_k, int64_t max_q, int64_t max_k) {
+    int st = check_attn(dtype, E, max_q, max_k, QH, KH, B);
+    if (st) return st;
+    if (Tq < 0 || Tk < 0) return fail(ONIONOP_E_SHAPE, "%s: negative dimension", what);
+    if (Tq >= (1LL << 31) || Tk >= (1LL << 31)) return fail(ONIONOP_E_UNSUPPORTED, "%s: too many packed rows", what);
+    if (B > 0 && (!cu_q || !cu_k)) return fail(ONIONOP_E_NULL, "%s: NULL sequence offsets", what);
+    return ok();
+}
+
+static onionop::AttnArgs varlen_args(int64_t E, int64_t Tq, int64_t Tk, int64_t QH, int64_t KH, int64_t B,
+                                     const int32_t* cu_q, const int32_t* cu_k, int64_t max_q, int64_t max_k,
+                                     const void* q, const void* k, const void* v, int causal, float scale) {
+    onionop::AttnArgs a{};
+    a.E = E; a.QL = max_q; a.KL = max_k; a.QH = QH; a.KH = KH; a.B = B;
+    a.q = q; a.k = k; a.v = v; a.pair = nullptr; a.kpad = nullptr; a.causal = causal != 0; a.scale = scale;
+    a.cu_q = cu_q; a.cu_k = cu_k; a.Tq = Tq; a.Tk = Tk;
+    return a;
+}
+
+int onionop_flash_attn_varlen_fwd(void* stream, int dtype, int64_t E, int64_t Tq, int64_t Tk, int64_t QH,
+                                  int64_t KH, int64_t B, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int64_t max_seqlen_q, int64_t max_seqlen_k, const void* q, const void* k,
+                                  const void* v, int causal, float scale, void* o, float* ms, float* ls) {
+    const char* what = "flash_attention (varlen)";
+    int st = check_varlen(what, dtype, E, Tq, Tk, QH, KH, B, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k);
+    if (st) return st;
+    const bool any_q = Tq * QH > 0, any_k = Tk * KH > 0;
+    if ((any_q && (!q || !o || !ms || !ls)) || (any_q && any_k && (!k || !v)))
+        return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+        return fail(ONIONOP_E_SHAPE, "%s: q, k, v and o must be 16-byte aligned", what);
+    onionop::AttnArgs a = varlen_args(E, Tq, Tk, QH, KH, B, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                      q, k, v, causal, scale);
+    a.o = o; a.ms = ms; a.ls = ls;
+    if (!onionop::launch_attn_fwd((hipStream_t)stream, dtype, a))
+        return fail(ONIONOP_E_UNSUPPORTED, "%s: no kernel for %s E=%lld", what, dt_name(dtype), (long long)E);
+    return check_launch(what);
+}
+
+size_t onionop_flash_attn_varlen_bwd_workspace(int dtype, int64_t E, int64_t Tq, int64_t QH) {
+    (void)dtype; (void)E;
+    if (Tq <= 0 || QH <= 0) return 0;
+    return 2 * (size_t)Tq * (size_t)QH * sizeof(float) + 256;  // lse2 and delta per packed query row
+}
+
+int onionop_flash_attn_varlen_bwd(void* stream, int dtype, int64_t E, int64_t Tq, int64_t Tk, int64_t QH,
+                                  int64_t KH, int64_t B, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int64_t max_seqlen_q, int64_t max_seqlen_k, const void* dO, const void* o,
+                                  const float* ms, const float* ls, const void* q, const void* k, const void* v,
+                                  int causal, float scale, int qk_fp16, void* dq, void* dk, void* dv, void* workspace,
+                                  size_t workspace_bytes) {
+    const char* what = "∇flash_attention (varlen)";
+    int st = check_varlen(what, dtype, E, Tq, Tk, QH, KH, B, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k);
+    if (st) return st;
+    const bool any_q = Tq * QH > 0, any_k = Tk * KH > 0;
+    if ((any_q && (!dO || !o || !ms || !ls || !q || !dq)) || (any_k && (!k || !v || !dk || !dv)))
+        return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);
+    if (!aligned16(dO) || !aligned16(o) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dq) ||
+        !aligned16(dk) || !aligned16(dv))
+        return fail(ONIONOP_E_SHAPE, "%s: tensors must be 16-byte aligned", what);
+    const size_t need = onionop_flash_attn_varlen_bwd_workspace(dtype, E, Tq, QH);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(ONIONOP_E_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", what, need, workspace_bytes);
+    onionop::AttnArgs a = varlen_args(E, Tq, Tk, QH, KH, B, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                      q, k, v, causal, scale);
+    a.dO = dO; a.o_in = o; a.ms_in = ms; a.ls_in = ls; a.qk_fp16 = qk_fp16 != 0;
+    a.dq = dq; a.dk = dk; a.dv = dv; a.dpair = nullptr;
+    if (need > 0) {
+        uintptr_t base = (reinterpret_cast<uintptr_t>(workspace) + 255) & ~uintptr_t(255);
+        a.lse2 = reinterpret_cast<float*>(base);
+        a.delta = a.lse2 + (size_t)Tq * (size_t)QH;
+    }
+    if (!onionop::launch_attn_bwd((hipStream_t)stream, dtype, a, onionop::kBwdAll))
+        return fail(ONIONOP_E_UNSUPPORTED, "%s: no kernel for %s E=%lld", what, dt_name(dtype), (long long)E);
+    return check_launch(what);
+}
+
 // -------------------------------------------------------------------- softmax
 
 static int check_rows(const char* what, int dtype, int64_t n, int64_t rows) {

@@ -145,6 +145,47 @@ struct KpadBlock {
     __device__ __forceinline__ bool none() const { return (d[0] | d[1] | d[2] | d[3]) == 0u; }
 };
 
+// Packed variable-length sequences: sequence b is rows cu_q[b] .. cu_q[b+1] of every q
+// head's (Tq x E) slab (and of the per-query statistics), rows cu_k[b] .. cu_k[b+1] of
+// every k / v head's (Tk x E) slab.  cu_q == nullptr: dense (B, H, L, E) tensors.
+struct VarLen {
+    const int* cu_q;
+    const int* cu_k;
+    int Tq, Tk;
+};
+
+// Where the attention problem of sequence (batch) b sits: q rows of head h start at
+// qbase + h * qhs, k rows of head h at kbase + h * khs; QL / KL are its lengths.  Grids
+// are sized for the maxima QLmax / KLmax (the dense lengths); varlen offsets are clamped
+// into their tensors, so malformed offsets cannot move an access outside them.
+struct SeqRows {
+    int64_t qbase, kbase, qhs, khs;
+    int QL, KL;
+    __device__ __forceinline__ int64_t qrow(int h) const { return qbase + (int64_t)h * qhs; }
+    __device__ __forceinline__ int64_t krow(int h) const { return kbase + (int64_t)h * khs; }
+};
+__device__ __forceinline__ SeqRows seq_rows(const VarLen& vl, int b, int QH, int KH, int QLmax, int KLmax) {
+    SeqRows s;
+    if (vl.cu_q == nullptr) {
+        s.qbase = (int64_t)b * QH * QLmax;
+        s.kbase = (int64_t)b * KH * KLmax;
+        s.qhs = QLmax;
+        s.khs = KLmax;
+        s.QL = QLmax;
+        s.KL = KLmax;
+    } else {
+        const int q0 = min(max(vl.cu_q[b], 0), vl.Tq), q1 = min(max(vl.cu_q[b + 1], q0), vl.Tq);
+        const int k0 = min(max(vl.cu_k[b], 0), vl.Tk), k1 = min(max(vl.cu_k[b + 1], k0), vl.Tk);
+        s.qbase = __builtin_amdgcn_readfirstlane(q0);
+        s.kbase = __builtin_amdgcn_readfirstlane(k0);
+        s.qhs = vl.Tq;
+        s.khs = vl.Tk;
+        s.QL = __builtin_amdgcn_readfirstlane(min(q1 - q0, QLmax));
+        s.KL = __builtin_amdgcn_readfirstlane(min(k1 - k0, KLmax));
+    }
+    return s;
+}
+
 // Element type helpers for the float16-rounded Q/K of the reference backward.
 template <typename T, bool QK16>
 __device__ __forceinline__ T qk_round(T x) {

@@ -38,7 +38,8 @@ bool launch_attn_bwd(hipStream_t s, int dt, const AttnArgs& a, int stages) {
     if (a.B == 0 || a.QH == 0) return true;
     if (a.QL == 0) {  // no queries: dk = dv = 0
         if (!(stages & kBwdDkDv)) return true;
-        const int64_t bytes = (dt == 0 ? 4 : 2) * a.E * a.KL * a.KH * a.B;
+        const int64_t krows = a.cu_q ? a.KH * a.Tk : a.KL * a.KH * a.B;
+        const int64_t bytes = (dt == 0 ? 4 : 2) * a.E * krows;
         if (bytes > 0) {
             zero_bytes_kernel<<<dim3((unsigned)((bytes + 1023) / 1024)), dim3(256), 0, s>>>(a.dk, bytes);
             zero_bytes_kernel<<<dim3((unsigned)((bytes + 1023) / 1024)), dim3(256), 0, s>>>(a.dv, bytes);

@@ -23,6 +23,11 @@ struct AttnArgs {
     int qk_fp16;
     void *dq, *dk, *dv, *dpair;
     float *lse2, *delta;  // workspace: log2-domain log-sum-exp and rowsum(dO o), (B, QH, QL)
+    // Packed variable-length sequences (cu_q == nullptr: dense).  With them, B counts
+    // the sequences, QL / KL are the longest lengths (they size the grids), tensors are
+    // (QH, Tq, E) / (KH, Tk, E), statistics (QH, Tq), and cu_q / cu_k hold B + 1 offsets.
+    const int *cu_q = nullptr, *cu_k = nullptr;
+    int64_t Tq = 0, Tk = 0;
 };
 
 bool launch_attn_fwd(hipStream_t s, int dt, const AttnArgs& a);

@@ -18,7 +18,8 @@ Reference names -> here:
   NNop.llama_rope / _llama_rope / ∇llama_rope / LlamaRotaryEmbedding -> same names
 """
 from ._lib import LIB_PATH, NNopError, lib
-from .attention import _flash_attention, attention_scale, flash_attention, grad_flash_attention
+from .attention import (_flash_attention, _flash_attention_varlen, attention_scale, flash_attention,
+                        flash_attention_varlen, grad_flash_attention, grad_flash_attention_varlen)
 from .norms import _layer_norm, _rms_norm, grad_layer_norm, grad_rms_norm, layer_norm, rms_norm
 from .rope import LlamaRotaryEmbedding, _llama_rope, grad_llama_rope, llama_rope
 from .softmax import _online_softmax, grad_online_softmax, grad_online_softmax_pullback, online_softmax
@@ -26,6 +27,7 @@ from .softmax import _online_softmax, grad_online_softmax, grad_online_softmax_p
 __all__ = [
     "LIB_PATH", "NNopError", "lib",
     "flash_attention", "_flash_attention", "grad_flash_attention", "attention_scale",
+    "flash_attention_varlen", "_flash_attention_varlen", "grad_flash_attention_varlen",
     "online_softmax", "_online_softmax", "grad_online_softmax", "grad_online_softmax_pullback",
     "rms_norm", "_rms_norm", "grad_rms_norm",
     "layer_norm", "_layer_norm", "grad_layer_norm",

@@ -35,6 +35,12 @@ SIGNATURES = {
                                          _vp, _i, _f, _i, _vp, _vp, _vp, _sz]),
     "onionop_flash_attn_bwd_dq": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                        _vp, _i, _f, _i, _vp, _vp, _vp, _sz]),
+    "onionop_flash_attn_varlen_fwd": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
+                                           _vp, _vp, _vp, _i, _f, _vp, _vp, _vp]),
+    "onionop_flash_attn_varlen_bwd_workspace": (_sz, [_i, _i64, _i64, _i64]),
+    "onionop_flash_attn_varlen_bwd": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
+                                           _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp,
+                                           _sz]),
     "onionop_softmax_fwd": (_i, [_vp, _i, _i64, _i64, _vp, _vp]),
     "onionop_softmax_bwd": (_i, [_vp, _i, _i64, _i64, _vp, _vp, _vp]),
     "onionop_softmax_bwd_bwd": (_i, [_vp, _i, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),

@@ -136,3 +136,92 @@ def flash_attention(q, k, v, pair: Optional[torch.Tensor] = None, *, causal: boo
     """
     o, _, _ = _FlashAttentionFn.apply(q, k, v, pair, kpad_mask, bool(causal), bool(qk_fp16))
     return o
+
+
+# ---------------------------------------------------------------- packed variable length
+#
+# Packed sequences (no padding): q (QH, Tq, E) == Julia (E, Tq, QH), k / v (KH, Tk, E);
+# sequence b is rows cu_seqlens_q[b]:cu_seqlens_q[b+1] of q (and cu_seqlens_k of k / v);
+# ms, ls (QH, Tq).  The reference has only kpad_mask for variable lengths
+# (src/attention.jl:16,83-89); this form skips padded queries as well as padded keys.
+
+def _check_varlen(q, k, v, cu_q, cu_k):
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("packed q, k and v must be 3-dimensional (E, T, H) arrays")
+    QH, Tq, E = q.shape
+    KH, Tk, KE = k.shape
+    if E != KE:
+        raise ValueError(f"Embedding dim of Q `{E}` must be the same as of K `{KE}`.")
+    if k.shape != v.shape:
+        raise ValueError(f"Shapes of K `{jdims(k)}` and V `{jdims(v)}` must be the same.")
+    if E <= 0 or (E & (E - 1)) != 0:
+        raise ValueError("Only power-of-2 embedding dims are supported.")
+    if KH == 0 or QH % KH != 0:
+        raise ValueError(f"Number of query heads `{QH}` must be divisible by number of KV heads `{KH}`.")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k and v must share one element type")
+    for name, cu in (("cu_seqlens_q", cu_q), ("cu_seqlens_k", cu_k)):
+        if cu.dtype != torch.int32 or cu.dim() != 1 or cu.device != q.device:
+            raise ValueError(f"{name} must be a 1-dimensional int32 tensor on the device of q")
+    if cu_q.shape != cu_k.shape:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must have the same length (B + 1)")
+    return QH, Tq, E, KH, Tk, cu_q.shape[0] - 1
+
+
+def _flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqlen_k: int, *,
+                            causal: bool):
+    """Forward over packed sequences; returns (o, ms, ls)."""
+    q, k, v = (device_tensor(t, "flash_attention (varlen)") for t in (q, k, v))
+    QH, Tq, E, KH, Tk, B = _check_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k)
+    dt = dtype_code(q, "flash_attention (varlen)")
+    o = torch.empty_like(q)
+    ms = torch.empty((QH, Tq), dtype=torch.float32, device=q.device)
+    ls = torch.empty((QH, Tq), dtype=torch.float32, device=q.device)
+    _lib.check(_lib.lib().onionop_flash_attn_varlen_fwd(
+        stream_of(q), dt, E, Tq, Tk, QH, KH, B, ptr(cu_seqlens_q), ptr(cu_seqlens_k), int(max_seqlen_q),
+        int(max_seqlen_k), ptr(q), ptr(k), ptr(v), int(bool(causal)), attention_scale(E, q.dtype), ptr(o), ptr(ms),
+        ptr(ls)))
+    return o, ms, ls
+
+
+def grad_flash_attention_varlen(do, o, ms, ls, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int,
+                                max_seqlen_k: int, *, causal: bool, qk_fp16: bool = True):
+    """Backward over packed sequences; returns (dq, dk, dv)."""
+    q, k, v, o = (device_tensor(t, "∇flash_attention (varlen)") for t in (q, k, v, o))
+    do = device_tensor(do, "∇flash_attention (varlen)").to(q.dtype)
+    QH, Tq, E, KH, Tk, B = _check_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k)
+    if do.shape != q.shape or o.shape != q.shape:
+        raise ValueError("Δ and o must have the shape of q")
+    dt = dtype_code(q, "∇flash_attention (varlen)")
+    L = _lib.lib()
+    ws_bytes = L.onionop_flash_attn_varlen_bwd_workspace(dt, E, Tq, QH)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    _lib.check(L.onionop_flash_attn_varlen_bwd(
+        stream_of(q), dt, E, Tq, Tk, QH, KH, B, ptr(cu_seqlens_q), ptr(cu_seqlens_k), int(max_seqlen_q),
+        int(max_seqlen_k), ptr(do), ptr(o), ptr(ms), ptr(ls), ptr(q), ptr(k), ptr(v), int(bool(causal)),
+        attention_scale(E, q.dtype), int(bool(qk_fp16)), ptr(dq), ptr(dk), ptr(dv), ptr(ws), int(ws_bytes)))
+    return dq, dk, dv
+
+
+class _FlashAttentionVarlenFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, causal, qk_fp16):
+        o, ms, ls = _flash_attention_varlen(q, k, v, cu_q, cu_k, max_q, max_k, causal=causal)
+        ctx.save_for_backward(q, k, v, cu_q, cu_k, o, ms, ls)
+        ctx.max_q, ctx.max_k, ctx.causal, ctx.qk_fp16 = max_q, max_k, causal, qk_fp16
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, cu_q, cu_k, o, ms, ls = ctx.saved_tensors
+        dq, dk, dv = grad_flash_attention_varlen(do.contiguous(), o, ms, ls, q, k, v, cu_q, cu_k, ctx.max_q,
+                                                 ctx.max_k, causal=ctx.causal, qk_fp16=ctx.qk_fp16)
+        return dq, dk, dv, None, None, None, None, None, None
+
+
+def flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqlen_k: int, *,
+                           causal: bool, qk_fp16: bool = True):
+    """Flash attention over packed variable-length sequences (differentiable in q, k, v)."""
+    return _FlashAttentionVarlenFn.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
+                                         int(max_seqlen_k), bool(causal), bool(qk_fp16))
