@@ -54,8 +54,7 @@ bool launch_rope(hipStream_t s, int dt, int64_t E, int64_t L, int64_t QH, int64_
 int64_t max_row_elems(int dt);
 // Number of workgroups (= float32 partial rows in the workspace) of the norm backward.
 int64_t norm_bwd_groups(int64_t rows, int64_t n);
-// float32 workspace elements per weight gradient of the norm backward (partial rows
-// plus the column-sum stage rows).
+// float32 workspace elements per weight gradient of the norm backward (partial rows).
 int64_t norm_bwd_ws_floats(int64_t rows, int64_t n);
 
 }  // namespace onionop

@@ -10,7 +10,7 @@
 // while it reduces and stores the current ones, so reads and writes of neighbouring rows
 // overlap.  Per-element weights stay in registers across rows, and the
 // backward's weight-gradient partials accumulate in registers, one float32 partial row
-// per workgroup, summed by a two-stage column reduction with a fixed order.
+// per workgroup, summed by one column-reduction launch with a fixed order.
 // All row accesses are buffer loads / stores over a resource that ends at the row's
 // last element: tails read zero and drop their stores without branches.
 #include <type_traits>
@@ -643,56 +643,41 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
 }
 
 // ------------------------------------------------------------------ column sums
-// The weight gradients are column sums of `groups` float32 partial rows (one matrix per
-// gradient, `count` of them).  Stage 1: block (x, y, z) sums partial rows
-// [kColChunk y, +kColChunk) of matrix z for 256 columns into stage row y; stage 2 sums
-// the stage rows of each column in order and converts to the output type.  Both the
-// blocking and the order are fixed, so the bits do not depend on the device.
-constexpr int kColChunk = 16;
+// The weight gradients are column sums of `groups` (at most 1024) float32 partial rows,
+// one matrix per gradient, `count` of them.  One launch: block (x, y) owns 64 columns of
+// matrix y; thread (column c, row group rg < 16) sums partial rows rg, rg + 16, ... in
+// order, sixteen loads in flight per batch, and the 16 row-group sums of a column then
+// combine in LDS by a fixed pairwise tree.  Blocking and order are fixed, so the bits do
+// not depend on the device.
+constexpr int kColRG = 16;
 
-__global__ __launch_bounds__(256) void colsum_stage1_kernel(const float* __restrict__ ws, int64_t groups, int64_t n,
-                                                            float* __restrict__ st, int64_t nst) {
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t g0 = (int64_t)blockIdx.y * kColChunk;
-    const int cnt = (int)(groups - g0 < kColChunk ? groups - g0 : kColChunk);
-    const rsrc_t r = make_rsrc(ws + (int64_t)blockIdx.z * groups * n, (uint32_t)(groups * n * 4));
-    // all kColChunk loads in flight at once; rows past `groups` or columns past n read 0
-    float v[kColChunk];
-#pragma unroll
-    for (int i = 0; i < kColChunk; ++i) {
-        const bool ok = i < cnt && e < n;
-        v[i] = bload_f32(r, ok ? (uint32_t)((g0 + i) * n + e) * 4u : 0xFFFFFFF0u);
-    }
-#pragma unroll
-    for (int w = 1; w < kColChunk; w *= 2)  // fixed pairwise tree
-#pragma unroll
-        for (int i = 0; i < kColChunk; i += 2 * w) v[i] += v[i + w];
-    if (e < n) st[((int64_t)blockIdx.z * nst + blockIdx.y) * n + e] = v[0];
-}
-
-// 64 columns per block; the 4 waves take stage rows w, w + 4, ... and combine in order.
-__global__ __launch_bounds__(256) void colsum_stage2_kernel(const float* __restrict__ st, int64_t nst, int64_t n,
-                                                            void* __restrict__ out0, void* __restrict__ out1, int dt) {
-    __shared__ float part[4][64];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
-    const float* src = st + (int64_t)blockIdx.y * nst * n + e;
+__global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ ws, int64_t groups, int64_t n,
+                                                      void* __restrict__ out0, void* __restrict__ out1, int dt) {
+    __shared__ float part[kColRG][64];
+    const int c = threadIdx.x & 63, rg = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + c;
+    const rsrc_t r = make_rsrc(ws + (int64_t)blockIdx.y * groups * n, (uint32_t)(groups * n * 4));
     float s = 0.f;
-    if (e < n) {
-        float a[8];
-        int64_t i = w;
-        for (; i + 28 < nst; i += 32) {
+    for (int64_t g0 = rg; g0 < groups; g0 += kColRG * 16) {
+        float v[16];  // partial rows g0 + 16 j; rows past `groups` or columns past n read 0
 #pragma unroll
-            for (int j = 0; j < 8; ++j) a[j] = src[(i + 4 * j) * n];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s += a[j];
+        for (int j = 0; j < 16; ++j) {
+            const int64_t row = g0 + 16 * j;
+            const bool ok = row < groups && e < n;
+            v[j] = bload_f32(r, ok ? (uint32_t)(row * n + e) * 4u : 0xFFFFFFF0u);
         }
-        for (; i < nst; i += 4) s += src[i * n];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s += v[j];
     }
-    part[w][lane] = s;
+    part[rg][c] = s;
     __syncthreads();
-    if (w != 0 || e >= n) return;
-    s = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+#pragma unroll
+    for (int w = 1; w < kColRG; w *= 2) {
+        if (rg % (2 * w) == 0) part[rg][c] += part[rg + w][c];
+        __syncthreads();
+    }
+    if (rg != 0 || e >= n) return;
+    s = part[0][c];
     void* out = blockIdx.y == 0 ? out0 : out1;
     if (dt == 0) reinterpret_cast<float*>(out)[e] = s;
     else if (dt == 1) reinterpret_cast<f16*>(out)[e] = from_f32<f16>(s);
@@ -870,23 +855,13 @@ int64_t norm_bwd_groups(int64_t rows, int64_t n) {
     return rows < g ? rows : g;
 }
 
-static int64_t colsum_stage_rows(int64_t groups) { return (groups + kColChunk - 1) / kColChunk; }
+int64_t norm_bwd_ws_floats(int64_t rows, int64_t n) { return norm_bwd_groups(rows, n) * n; }
 
-int64_t norm_bwd_ws_floats(int64_t rows, int64_t n) {
-    const int64_t g = norm_bwd_groups(rows, n);
-    return (g + colsum_stage_rows(g)) * n;
-}
-
-// Column sums of `count` partial matrices at ws ([count][groups][n]) into out0 / out1,
-// with the stage rows after them ([count][nst][n]).
+// Column sums of `count` partial matrices at ws ([count][groups][n]) into out0 / out1.
 static void colsum(hipStream_t s, float* ws, int64_t groups, int64_t n, int count, void* out0, void* out1,
                    int dt) {
-    const int64_t nst = colsum_stage_rows(groups);
-    float* st = ws + (int64_t)count * groups * n;
-    const unsigned cx = (unsigned)((n + 255) / 256);
-    colsum_stage1_kernel<<<dim3(cx, (unsigned)nst, (unsigned)count), dim3(256), 0, s>>>(ws, groups, n, st, nst);
-    colsum_stage2_kernel<<<dim3((unsigned)((n + 63) / 64), (unsigned)count), dim3(256), 0, s>>>(st, nst, n, out0,
-                                                                                               out1, dt);
+    colsum_kernel<<<dim3((unsigned)((n + 63) / 64), (unsigned)count), dim3(1024), 0, s>>>(ws, groups, n, out0, out1,
+                                                                                         dt);
 }
 
 bool launch_softmax_fwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* x, void* y) {

@@ -50,11 +50,10 @@ def test_workspace_queries_are_host_only():
     L = nnop.lib()
     assert L.onionop_flash_attn_bwd_workspace(2, 64, 4096, 4096, 4, 4, 4) >= 2 * 4096 * 16 * 4
     assert L.onionop_flash_attn_bwd_workspace(2, 64, 0, 4096, 4, 4, 4) == 0
-    # rows of 4096 elements: 256 float32 partial rows, then ceil(256 / 16) column-sum stage rows
-    assert L.onionop_rms_norm_bwd_workspace(4096, 16384) == (256 + 16) * 4096 * 4
-    # rows of 512 elements: 1024 partial rows, then 64 stage rows
-    assert L.onionop_rms_norm_bwd_workspace(512, 16384) == (1024 + 64) * 512 * 4
-    assert L.onionop_layer_norm_bwd_workspace(4096, 3) == 2 * (3 + 1) * 4096 * 4
+    # rows of 4096 elements: 256 float32 partial rows; rows of 512 elements: 1024
+    assert L.onionop_rms_norm_bwd_workspace(4096, 16384) == 256 * 4096 * 4
+    assert L.onionop_rms_norm_bwd_workspace(512, 16384) == 1024 * 512 * 4
+    assert L.onionop_layer_norm_bwd_workspace(4096, 3) == 2 * 3 * 4096 * 4
 
 
 def test_c_abi_validation_errors():
