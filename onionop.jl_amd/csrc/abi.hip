@@ -63,6 +63,15 @@ int check_attn(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t
     return ok();
 }
 
+// The bias kernels address 64 key rows of one (batch, head) bias slice with 32-bit byte
+// offsets.
+int check_pair(const void* pair, int dtype, int64_t QL, int64_t QH) {
+    if (pair != nullptr && 64 * QL * QH * (int64_t)dt_size(dtype) >= (1LL << 32))
+        return fail(ONIONOP_E_UNSUPPORTED,
+                    "flash_attention: pair bias too large (64*QL*QH*sizeof(T) must be below 2^32 bytes)");
+    return ok();
+}
+
 std::mutex g_lds_mu;
 size_t g_lds[64];
 bool g_lds_set[64];
@@ -97,6 +106,7 @@ int onionop_flash_attn_fwd(void* stream, int dtype, int64_t E, int64_t QL, int64
                            const uint8_t* kpad, int causal, float scale, void* o, float* ms, float* ls) {
     int st = check_attn(dtype, E, QL, KL, QH, KH, B);
     if (st) return st;
+    if ((st = check_pair(pair, dtype, QL, QH))) return st;
     const bool any_q = QL * QH * B > 0, any_k = KL * KH * B > 0;
     if ((any_q && (!q || !o || !ms || !ls)) || (any_q && any_k && (!k || !v)))
         return fail(ONIONOP_E_NULL, "flash_attention: NULL tensor pointer");
@@ -127,6 +137,7 @@ static int attn_bwd_common(const char* what, int stages, void* stream, int dtype
                            void* dpair, void* workspace, size_t workspace_bytes) {
     int st = check_attn(dtype, E, QL, KL, QH, KH, B);
     if (st) return st;
+    if ((st = check_pair(pair, dtype, QL, QH))) return st;
     const bool any_q = QL * QH * B > 0, any_k = KL * KH * B > 0;
     if (stages & onionop::kBwdPre) {
         if (any_q && (!dO || !o || !ms || !ls)) return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);

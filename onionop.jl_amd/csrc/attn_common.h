@@ -145,6 +145,88 @@ struct KpadBlock {
     __device__ __forceinline__ bool none() const { return (d[0] | d[1] | d[2] | d[3]) == 0u; }
 };
 
+// ---------------------------------------------------------------- pair bias
+// The bias tensor is (B, KL, QL, QH) row-major == Julia (QH, QL, KL, B): element
+// (b, key, query, head) at ((b KL + key) QL + query) QH + head.  The heads of one
+// (key, query) are adjacent, so no two elements a lane needs are: every element is its
+// own 16/32-bit buffer access.  The loads are unconditional (offsets past the resource
+// read 0) and keep raw bits in registers until the scores use them, so a block's loads
+// issue back to back and are prefetched a tile ahead.  Offsets are 32-bit: the host
+// requires 64 QL QH sizeof(T) < 2^32 (a resource spans at most 64 key rows).
+
+// Raw bits of the element of type T at byte offset off (0 past the resource).
+template <typename T>
+__device__ __forceinline__ uint32_t bload_bits(rsrc_t r, uint32_t off) {
+    if constexpr (sizeof(T) == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+    else return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+template <typename T>
+__device__ __forceinline__ float bits_f32(uint32_t u) {
+    if constexpr (sizeof(T) == 4) return __uint_as_float(u);
+    else if constexpr (__is_same(T, bf16)) return __uint_as_float(u << 16);
+    else return (float)__builtin_bit_cast(f16, (unsigned short)u);
+}
+// Store x as T at byte offset off (dropped past the resource).
+template <typename T>
+__device__ __forceinline__ void bstore_elem(rsrc_t r, uint32_t off, float x) {
+    if constexpr (sizeof(T) == 4) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, (int)off, 0, 0);
+    } else {
+        const T t = from_f32<T>(x);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, t), r, (int)off, 0, 0);
+    }
+}
+
+// Resource over the bias of rows [k0, k0 + nrows) of batch b, head `head`: the byte
+// offset of (key k0 + i, query j) is (i QL + j) QH sizeof(T).  Rows past KL read 0.
+template <typename T>
+__device__ __forceinline__ rsrc_t pair_rsrc(const T* pair, int b, int k0, int nrows, int KL, int QL, int QH, int head) {
+    const int rows = max(0, min(nrows, KL - k0));
+    const uint32_t bytes = rows > 0 ? ((uint32_t)rows * (uint32_t)QL * (uint32_t)QH - (uint32_t)head) * sizeof(T) : 0u;
+    return make_rsrc(pair + (((int64_t)b * KL + k0) * QL) * QH + head, bytes);
+}
+
+// Byte offsets of one lane's 16 elements of a 32 x 32 C block, rows crow(r, h):
+//  query lane (S^T tiles: lane = query q, rows = keys kbl + crow(r, h) of the resource)
+//    ((kbl + crow(r, h)) QL + q) QH sizeof(T);
+//  key lane (S tiles: lane = key kl of the resource, rows = queries qb + crow(r, h))
+//    (kl QL + qb + crow(r, h)) QH sizeof(T).
+template <typename T>
+__device__ __forceinline__ uint32_t pair_off_q(int kbl, int r, int q, int h, int QL, int QH) {
+    return ((uint32_t)(kbl + crow(r, h)) * (uint32_t)QL + (uint32_t)q) * (uint32_t)QH * sizeof(T);
+}
+template <typename T>
+__device__ __forceinline__ uint32_t pair_off_k(int kl, int qb, int r, int h, int QL, int QH) {
+    return ((uint32_t)kl * (uint32_t)QL + (uint32_t)(qb + crow(r, h))) * (uint32_t)QH * sizeof(T);
+}
+
+// The bias bits of one lane's 16 rows of a 32 x 32 block.
+template <typename T>
+struct PairBlock {
+    uint32_t u[16];
+    __device__ __forceinline__ void load_q(rsrc_t rs, int kbl, int q, int h, int QL, int QH) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) u[r] = bload_bits<T>(rs, pair_off_q<T>(kbl, r, q, h, QL, QH));
+    }
+    __device__ __forceinline__ void load_k(rsrc_t rs, int kl, int qb, int h, int QL, int QH) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) u[r] = bload_bits<T>(rs, pair_off_k<T>(kl, qb, r, h, QL, QH));
+    }
+    __device__ __forceinline__ float get(int r) const { return bits_f32<T>(u[r]); }
+};
+
+// Workgroups are dispatched round-robin over the 8 XCDs (block x runs on XCD x % 8),
+// and each XCD has its own L2.  xcd_group renumbers the n blocks of a grid so that G
+// consecutive logical indices run on one XCD and successive groups of G on successive
+// XCDs; a tail of fewer than 8 G blocks keeps the plain order.  With G = the heads of
+// one (batch, tile), the heads that share every bias cache line share one L2.
+__device__ __forceinline__ int xcd_group(int x, int G, int n) {
+    const int round = 8 * G, full = n - n % round;
+    if (x >= full) return x;
+    const int j = x >> 3;
+    return (j / G) * round + (x & 7) * G + j % G;
+}
+
 // Packed variable-length sequences: sequence b is rows cu_q[b] .. cu_q[b+1] of every q
 // head's (Tq x E) slab (and of the per-query statistics), rows cu_k[b] .. cu_k[b+1] of
 // every k / v head's (Tk x E) slab.  cu_q == nullptr: dense (B, H, L, E) tensors.

@@ -75,6 +75,9 @@ def test_c_abi_validation_errors():
     st = L.onionop_flash_attn_bwd(None, 2, 64, 8, 8, 2, 2, 1, 16, 16, 16, 16, 16, 16, 16, None, None, 0, 1.0, 0,
                                   16, 16, 16, None, 16, 8)
     assert st == -6
+    # a bias slice whose 64-key-row span needs offsets of 2^32 bytes or more
+    st = L.onionop_flash_attn_fwd(None, 0, 16, 1 << 20, 8, 64, 64, 1, 16, 16, 16, 16, None, 0, 1.0, 16, 16, 16)
+    assert st == -3 and b"pair bias too large" in L.onionop_last_error()
     st = L.onionop_llama_rope(None, 2, 15, 4, 1, 1, 1, 16, 16, 16, 16, 1.0, 16, 16)
     assert st == -1
     st = L.onionop_softmax_fwd(None, 0, 1 << 20, 4, 16, 16)
