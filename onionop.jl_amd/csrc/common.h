@@ -113,17 +113,39 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 }
 
 // ---------------------------------------------------------------- reductions
+// Wave-wide sum / max with the result in every lane, all in VALU (no LDS crossbar round
+// trips): DPP lane permutations within rows of 16 -- quad_perm [1,0,3,2] (lane ^ 1),
+// quad_perm [2,3,0,1] (lane ^ 2), row_half_mirror (lane i with 7 - i of each 8, which after
+// the two quad steps pairs the two quads of every 8) and row_mirror (i with 15 - i: the two
+// halves of every 16) -- then v_permlane16_swap (the two rows of every 32) and
+// v_permlane32_swap (the two halves of the wave).  Each step combines two equal partial
+// results in an order that is the same in every lane, so all lanes end bit-identical.
+// Every lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_perm(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float pair16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-    v = pair32_sum(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    v += dpp_perm<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_perm<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_perm<0x141>(v);  // row_half_mirror
+    v += dpp_perm<0x140>(v);  // row_mirror
+    return pair32_sum(pair16_sum(v));
 }
 __device__ __forceinline__ float wave_max(float v) {
-    v = pair32_max(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    v = fmaxf(v, dpp_perm<0xB1>(v));
+    v = fmaxf(v, dpp_perm<0x4E>(v));
+    v = fmaxf(v, dpp_perm<0x141>(v));
+    v = fmaxf(v, dpp_perm<0x140>(v));
+    return pair32_max(pair16_max(v));
 }
 
 // Block-wide sum of up to 16 waves; every thread gets the result.  `red` must hold

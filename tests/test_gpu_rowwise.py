@@ -147,6 +147,21 @@ def test_layer_norm_f32(dev, case):
            "dx": rel_err(host(dx), dx_r), "dw": rel_err(host(dw), dw_r), "db": rel_err(host(db), db_r)}, 1e-5)
 
 
+@pytest.mark.parametrize("emb", [513, 4096])
+def test_layer_norm_large_mean(dev, emb):
+    """x = 1000 + U[0,1): the variance is 1e-7 of E[x^2], so E[x^2] - mean^2 in float32 would
+    lose it entirely; the two-pass statistics keep rstd to float32 rounding of the mean."""
+    rng = np.random.default_rng(emb)
+    x, xn = make(rng, (16, emb), torch.float32, dev, kind="uniform", offset=1000.0)
+    w, wn = make(rng, (emb,), torch.float32, dev, kind="uniform")
+    b, bn = make(rng, (emb,), torch.float32, dev, kind="uniform")
+    y, mu, rstd = nnop._layer_norm(x, w, b)
+    torch.cuda.synchronize()
+    y_r, mu_r, r_r = oracle.layer_norm_fwd(xn, wn, bn)
+    check({"mu": rel_err(host(mu), mu_r), "rstd": rel_err(host(rstd), r_r)}, 1e-4)
+    check({"y": rel_err(host(y), y_r)}, 1e-3)  # x - mu carries the float32 rounding of mu (ulp 6e-5)
+
+
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("emb,n", [(4096, 64), (1024, 3000)])
 def test_layer_norm_16bit(dev, dt, emb, n):
