@@ -165,10 +165,10 @@ struct TileDMA {
 };
 
 // Zero columns [E, DS) of two NR-row LDS tiles (the padding read as rows E..31 of a 32-row
-// MFMA block when E = 16).
+// MFMA block when E = 16); `t` is this thread's index among the NT threads that share them.
 template <typename T, int NR, int E, int DS, int NT>
-__device__ __forceinline__ void zero_pad_cols(T* a, T* b) {
-    for (int i = threadIdx.x; i < NR * (DS - E); i += NT) {
+__device__ __forceinline__ void zero_pad_cols(T* a, T* b, int t) {
+    for (int i = t; i < NR * (DS - E); i += NT) {
         const int row = i / (DS - E), col = E + i % (DS - E);
         a[row * DS + col] = (T)0.f;
         b[row * DS + col] = (T)0.f;

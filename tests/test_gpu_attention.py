@@ -79,6 +79,14 @@ CASES = [
     ("bf16", 64, 256, 256, 2, 2, 3, True, True, True),
     ("bf16", 128, 512, 512, 4, 1, 2, True, False, False),
     ("bf16", 128, 257, 257, 8, 2, 2, False, False, True),
+    # 16-bit bias, QH % 4 == 0 and >= 192 four-head forward workgroups (q tiles x QH/4 x B):
+    # four heads per forward workgroup, bias records staged through LDS
+    ("bf16", 64, 64, 257, 32, 8, 24, True, True, True),
+    ("f16", 16, 100, 300, 16, 16, 24, False, True, False),
+    ("bf16", 32, 130, 129, 12, 4, 22, False, True, True),
+    # the same kind of bias with fewer workgroups: one head per workgroup
+    ("bf16", 64, 511, 257, 4, 2, 2, True, True, True),
+    ("bf16", 32, 200, 200, 12, 4, 1, False, True, False),
 ]
 
 
