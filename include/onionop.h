@@ -75,6 +75,9 @@ int onionop_device_lds_bytes(int device, size_t* bytes_out /* host pointer */);
  * scale multiplies Q.K before the bias; the reference passes T(1/sqrt(E))
  * (src/attention.jl:166).  E must be a power of two in {16, 32, 64, 128};
  * QH % KH == 0 (q head j uses kv head j / (QH/KH), src/attention.jl:36).
+ * Limits of this build (ONIONOP_E_UNSUPPORTED beyond them): L * E * sizeof(T) < 2^31
+ * bytes per (head, batch) slice of q/k/v, and with a bias 64 * QL * QH * sizeof(T) < 2^32
+ * (the kernels address 64 key rows of one bias slice with 32-bit offsets).
  * Rows whose keys are all masked give o = 0, ms = -Inf, ls = 0 (the reference
  * produces NaN there).
  */
