@@ -84,6 +84,9 @@ CASES = [
     ("bf16", 64, 64, 257, 32, 8, 24, True, True, True),
     ("f16", 16, 100, 300, 16, 16, 24, False, True, False),
     ("bf16", 32, 130, 129, 12, 4, 22, False, True, True),
+    # ... and QH == KH: four kv heads per dK/dV workgroup as well
+    ("bf16", 32, 200, 257, 8, 8, 24, True, True, True),
+    ("f16", 64, 128, 130, 4, 4, 64, True, True, False),
     # the same kind of bias with fewer workgroups: one head per workgroup
     ("bf16", 64, 511, 257, 4, 2, 2, True, True, True),
     ("bf16", 32, 200, 200, 12, 4, 1, False, True, False),
