@@ -227,6 +227,34 @@ __device__ __forceinline__ int xcd_group(int x, int G, int n) {
     return (j / G) * round + (x & 7) * G + j % G;
 }
 
+// (rank, batch, q head) of block x of a query-tile grid of ranks x NB x QH blocks.  Plain
+// order: the rank varies slowest, (batch, q head) fastest.  With GQA (rep = QH / KH > 1)
+// and NB KH a multiple of 8, each XCD (block x runs on XCD x % 8) instead takes whole
+// (batch, kv head) pairs, the rep q heads of a pair next to each other, still rank by
+// rank: an XCD's L2 then serves the K/V of NB KH / 8 pairs to all their q heads, instead
+// of the K/V of up to 8 times as many pairs to one q head each.
+struct QBlock {
+    int rank, b, qh;
+};
+__device__ __forceinline__ QBlock qblock_map(int x, int QH, int KH, int NB) {
+    QBlock r;
+    const int rep = QH / KH, pairs = NB * KH;
+    if (rep > 1 && (pairs & 7) == 0) {
+        const int xcd = x & 7, j = x >> 3, per = pairs >> 3;
+        const int jq = j % rep, t = j / rep;
+        const int p = (t % per) * 8 + xcd;
+        r.rank = t / per;
+        r.b = p / KH;
+        r.qh = (p % KH) * rep + jq;
+    } else {
+        const int BH = QH * NB, bh = x % BH;
+        r.rank = x / BH;
+        r.b = bh / QH;
+        r.qh = bh % QH;
+    }
+    return r;
+}
+
 // Packed variable-length sequences: sequence b is rows cu_q[b] .. cu_q[b+1] of every q
 // head's (Tq x E) slab (and of the per-query statistics), rows cu_k[b] .. cu_k[b+1] of
 // every k / v head's (Tk x E) slab.  cu_q == nullptr: dense (B, H, L, E) tensors.
