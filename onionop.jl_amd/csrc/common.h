@@ -96,9 +96,18 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // max / sum over lanes l and l ^ 32, by v_permlane32_swap (no LDS round trip).  With
 // x in both operands the swap returns the low half broadcast to both halves and the
 // high half broadcast to both halves; every lane combines the two.
+// max(a, b) as one v_max_f32.  fmaxf of values the compiler cannot prove canonical (MFMA
+// results, values read across lanes, loop-carried values) costs two extra canonicalising
+// v_max_f32 under IEEE mode; the operands here are never signalling NaNs.  Not volatile,
+// so the scheduler still moves it.
+__device__ __forceinline__ float fmax2(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ float pair32_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return fmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float pair32_sum(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
