@@ -93,9 +93,6 @@ static __global__ void fill_zero_kernel(void* p, int64_t bytes) {
 // for results below 2^-126; those may come back as 0, which softmax weights tolerate.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// max / sum over lanes l and l ^ 32, by v_permlane32_swap (no LDS round trip).  With
-// x in both operands the swap returns the low half broadcast to both halves and the
-// high half broadcast to both halves; every lane combines the two.
 // max(a, b) as one v_max_f32.  fmaxf of values the compiler cannot prove canonical (MFMA
 // results, values read across lanes, loop-carried values) costs two extra canonicalising
 // v_max_f32 under IEEE mode; the operands here are never signalling NaNs.  Not volatile,
@@ -105,6 +102,10 @@ __device__ __forceinline__ float fmax2(float a, float b) {
     asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
 }
+
+// max / sum over lanes l and l ^ 32, by v_permlane32_swap (no LDS round trip).  With
+// x in both operands the swap returns the low half broadcast to both halves and the
+// high half broadcast to both halves; every lane combines the two.
 __device__ __forceinline__ float pair32_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));

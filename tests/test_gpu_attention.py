@@ -79,6 +79,10 @@ CASES = [
     ("bf16", 64, 256, 256, 2, 2, 3, True, True, True),
     ("bf16", 128, 512, 512, 4, 1, 2, True, False, False),
     ("bf16", 128, 257, 257, 8, 2, 2, False, False, True),
+    # 16-bit E = 128 dK / dV on two waves per key slice: causal with QL != KL and key
+    # padding; a single partial key tile with more queries than keys
+    ("bf16", 128, 200, 333, 4, 2, 2, True, False, True),
+    ("f16", 128, 96, 64, 2, 1, 3, True, False, False),
     # 16-bit bias, QH % 4 == 0 and >= 192 four-head forward workgroups (q tiles x QH/4 x B):
     # four heads per forward workgroup, bias records staged through LDS
     ("bf16", 64, 64, 257, 32, 8, 24, True, True, True),

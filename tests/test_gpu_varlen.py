@@ -65,6 +65,7 @@ CASES = [
     ("bf16", 64, 4, 4, [300, 1, 64, 129, 0, 257], [300, 1, 64, 129, 0, 257], True),
     ("bf16", 64, 4, 2, [500, 37, 1000], [500, 37, 1000], False),
     ("bf16", 128, 8, 2, [255, 512, 33], [255, 512, 33], True),
+    ("f16", 128, 4, 4, [40, 300, 97], [260, 5, 97], False),
     ("f16", 32, 2, 2, [100, 200, 3], [150, 7, 300], False),
     ("f16", 64, 2, 1, [63, 65, 1, 128], [63, 65, 1, 128], True),
     ("f32", 64, 2, 2, [70, 0, 190], [70, 0, 190], True),
