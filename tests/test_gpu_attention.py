@@ -68,6 +68,9 @@ CASES = [
     ("f32", 64, 1024, 1024, 2, 2, 1, False, False, True),
     ("f32", 128, 257, 257, 4, 2, 2, True, False, False),
     ("f32", 64, 511, 511, 2, 2, 3, True, True, True),
+    # float32 on a small grid: two-wave dK/dV and one-wave dQ, four groups each, with
+    # causal GQA, key padding and QL != KL
+    ("f32", 64, 300, 200, 3, 1, 2, True, False, True),
     ("f16", 16, 256, 256, 2, 2, 3, False, True, True),
     ("f16", 32, 511, 255, 2, 2, 3, False, False, True),
     ("f16", 64, 512, 512, 2, 2, 3, True, True, False),
@@ -118,6 +121,12 @@ def test_gqa_parity(dev, dt, case):
 def test_fp32_qk_fp16_mode(dev, causal):
     """The reference backward's Float16 Q/K (src/attention_bwd.jl:20-21), reproduced."""
     run_case(dev, "f32", 64, 300, 300, 2, 2, 2, causal, True, False, seed=3, qk16=True)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_fp32_qk_fp16_mode_no_bias(dev, causal):
+    """The same without a bias: the two-wave dK/dV and one-wave dQ kernels round Q/K too."""
+    run_case(dev, "f32", 64, 300, 300, 2, 2, 2, causal, False, False, seed=5, qk16=True)
 
 
 def test_fully_masked_rows(dev):
