@@ -138,6 +138,17 @@ def test_fully_masked_rows(dev):
         run_case(dev, dt, 32, 70, 130, 2, 2, 2, False, True, True, seed=5, kpad=kpad)
 
 
+@pytest.mark.parametrize("dt,E", [("f32", 64), ("bf16", 128), ("bf16", 64)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_padded_key_blocks(dev, dt, E, causal):
+    """Whole 32- and 64-key blocks of padding (workgroups whose every key is padded write
+    zero dK / dV without computing), next to partly padded blocks."""
+    kpad = np.ones((2, 200), dtype=bool)
+    kpad[0, 64:160] = False
+    kpad[1, 150:] = False
+    run_case(dev, dt, E, 180, 200, 4, 2, 2, causal, False, True, seed=11, kpad=kpad)
+
+
 def test_single_key(dev):
     """L = 1: o = v exactly, whatever q."""
     rng = np.random.default_rng(1)
