@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 
 MI355X_BF16_DENSE_TFLOPS = 2500.0   # dense bf16/fp16 MFMA peak
 MI355X_HBM_GBS = 8000.0             # HBM3E peak
+MI355X_FP32_MFMA_TFLOPS = 157.3     # dense fp32 MFMA peak
 
 METRIC = "flash-attn fwd+bwd TFLOP/s (bf16, L=4096) + norm/softmax HBM GB/s"
 
@@ -270,6 +271,76 @@ def cpu_baseline(E=64, L=4096, H=4, B=4, threads=None):
                       f"{dt:.1f} s"}
 
 
+def workload_timings(torch, nnop, dev):
+    """Steady-state fwd+bwd times of the three other attention workloads at full size, through
+    the nnop API (0.3 s warm, then HIP events): float32 (64,1024,4,2) non-causal with the
+    Float16 Q/K backward, bf16 pair bias (32,768,8,2), and RoPE + causal GQA (128,8192,32:8,4)
+    with per-sequence lengths in [1024, 8192] as a key mask, plus the RoPE backward.
+    One JSON line each; inputs are not rotated (the 18.9 MB bias can sit in the MALL)."""
+    import numpy as np
+
+    def steady(f, iters):
+        t0 = time.time()
+        while time.time() - t0 < 0.3:
+            f()
+        torch.cuda.synchronize()
+        return time_region(torch, f, iters) * 1e3  # us
+
+    g = torch.Generator(device="cpu").manual_seed(0)
+    E, L, H, B = 64, 1024, 4, 2
+    q, k, v = [torch.rand((B, H, L, E), generator=g).to(dev) for _ in range(3)]
+    do = torch.ones_like(q)
+
+    def f32_step():
+        o, ms, ls = nnop._flash_attention(q, k, v, causal=False)
+        nnop.grad_flash_attention(do, o, ms, ls, q, k, v, causal=False, qk_fp16=True)
+
+    t = steady(f32_step, 50)
+    fl = 14 * B * H * L * L * E
+    print(json.dumps({"workload": "flash_attention fwd+bwd f32 (64,1024,4,2) non-causal, Float16 Q/K backward",
+                      "us": round(t, 1), "TFLOP/s": round(fl / t / 1e6, 1),
+                      "frac_of_fp32_mfma": round(fl / t / 1e6 / MI355X_FP32_MFMA_TFLOPS, 3)}), flush=True)
+
+    E, L, H, B = 32, 768, 8, 2
+    q, k, v, do = [torch.randn((B, H, L, E), generator=g).to(torch.bfloat16).to(dev) for _ in range(4)]
+    pair = torch.randn((B, L, L, H), generator=g).to(torch.bfloat16).to(dev)
+
+    def pair_step():
+        o, ms, ls = nnop._flash_attention(q, k, v, pair, causal=False)
+        nnop.grad_flash_attention(do, o, ms, ls, q, k, v, pair, causal=False)
+
+    t = steady(pair_step, 50)
+    fl = 14 * B * H * L * L * E
+    # bias read by the forward and dK/dV, read and dpair written by dQ; q,k,v,o,dO,dq,dk,dv, o re-read
+    byt = 3 * pair.numel() * 2 + 9 * q.numel() * 2
+    print(json.dumps({"workload": "flash_attention fwd+bwd bf16 (32,768,8,2) non-causal, pair bias, grads incl. bias",
+                      "us": round(t, 1), "TFLOP/s": round(fl / t / 1e6, 1), "GB/s": round(byt / t / 1e3),
+                      "algorithmic_MB": round(byt / 1e6, 1)}), flush=True)
+
+    B, QH, KH, L, E = 4, 32, 8, 8192, 128
+    lens = np.random.default_rng(4).integers(1024, L + 1, size=B)
+    q = torch.randn((B, QH, L, E), generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn((B, KH, L, E), generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn((B, KH, L, E), generator=g).to(torch.bfloat16).to(dev)
+    cos, sin = nnop.LlamaRotaryEmbedding(E)(torch.arange(L, dtype=torch.float32)[None].expand(B, L))
+    cos, sin = cos.to(dev), sin.to(dev)
+    kp = torch.from_numpy(np.arange(L)[None, :] < lens[:, None]).to(dev)
+    do = torch.randn_like(q) * kp[:, None, :, None]
+
+    def gqa_step():
+        qr, kr = nnop._llama_rope(q, k, cos, sin, bwd=False)
+        o, ms, ls = nnop._flash_attention(qr, kr, v, causal=True, kpad_mask=kp)
+        dq, dk, dv, _ = nnop.grad_flash_attention(do, o, ms, ls, qr, kr, v, causal=True, kpad_mask=kp)
+        nnop._llama_rope(dq, dk, cos, sin, bwd=True)
+
+    t = steady(gqa_step, 5)
+    fl = 7 * QH * E * sum(int(n) ** 2 for n in lens)  # causal fwd+bwd over each sequence's valid keys
+    print(json.dumps({"workload": "llama_rope + flash_attention fwd+bwd bf16 (128,8192,32:8,4) causal GQA, "
+                      "key mask from per-sequence lengths, + llama_rope bwd", "lens": lens.tolist(),
+                      "us": round(t), "TFLOP/s_valid_work": round(fl / t / 1e6),
+                      "frac_of_bf16_peak": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 3)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -279,6 +350,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-memory", action="store_true", help="skip the HBM-bound kernel set")
+    ap.add_argument("--workloads", action="store_true",
+                    help="instead of the bench line, time the other attention workloads (float32, "
+                         "pair bias, RoPE + GQA) and print one JSON line each")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run 3 plain device copies of MIB MiB (a known-size kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -292,6 +366,9 @@ def main():
     import nnop
 
     dev = torch.device("cuda:0")
+    if args.workloads:
+        workload_timings(torch, nnop, dev)
+        return
     E, L, H, B = 64, 4096, 4, 4
     q, k, v, do = attention_setup(torch, nnop, dev, E, L, H, B)
     step = AttnStep(torch, nnop, q, k, v, do, causal=True)
