@@ -12,9 +12,16 @@ and layer norm fwd/bwd (bf16, emb 4096 x 16384), Llama RoPE fwd (bf16, q (128,81
 k (128,8192,8,4)), each over a rotating set of buffers larger than the 256 MB
 Infinity Cache, with algorithmic bytes (one read / write of each API tensor).
 
+Also reported (`workloads`): the other attention workloads at full size, timed through the
+C ABI (float32 (64,1024,4,2); bf16 pair bias (32,768,8,2); llama_rope + causal GQA
+(128,8192,32:8,4) with per-sequence lengths, as a key mask and packed).
+
+Before the counted warmup a settle phase runs the step until the GPU's clocks are steady
+(the clocks need ~30 ms of this load to ramp); its length is reported as settle_ms.
+
 `roofline` is the slowest kernel of the step, timed alone with HIP events on the stream
 the library launches on.  `cpu_baseline` is the oracle's float32 restatement of the
-reference algorithm (oracle/oracle.c, FAITHFUL mode) on the host cores.
+reference algorithm (oracle/oracle.c, FAITHFUL mode) on the host cores this job may use.
 """
 from __future__ import annotations
 
@@ -49,62 +56,104 @@ def attention_setup(torch, nnop, dev, E=64, L=4096, H=4, B=4, seed=2):
 
 
 class AttnStep:
-    """One fwd+bwd step through the C ABI, with buffers allocated once."""
+    """One fwd+bwd step through the C ABI, with buffers allocated once.
 
-    def __init__(self, torch, nnop, q, k, v, do, causal=True):
+    q (B, QH, QL, E), k / v (B, KH, KL, E); pair (B, KL, QL, QH) and kpad (B, KL) bool are
+    optional.  qk16 is the backward's Float16 Q/K flag (float32 only)."""
+
+    def __init__(self, torch, nnop, q, k, v, do, causal=True, pair=None, kpad=None, qk16=0):
         from nnop import _lib
-        from nnop._util import ptr
+        from nnop._util import dtype_code, ptr
 
         self.torch, self.L, self.ptr = torch, _lib.lib(), ptr
-        self.q, self.k, self.v, self.do = q, k, v, do
+        self.q, self.k, self.v, self.do, self.pair, self.kpad = q, k, v, do, pair, kpad
         B, H, QL, E = q.shape
+        self.dt = dtype_code(q, "bench")
         self.dims = (E, QL, k.shape[2], H, k.shape[1], B)
-        self.causal = int(causal)
+        self.causal, self.qk16 = int(causal), int(qk16)
         self.scale = nnop.attention_scale(E, q.dtype)
         self.o = torch.empty_like(q)
         self.ms = torch.empty((B, H, QL), dtype=torch.float32, device=q.device)
         self.ls = torch.empty_like(self.ms)
         self.dq, self.dk, self.dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        self.wsb = int(self.L.onionop_flash_attn_bwd_workspace(2, *self.dims))
-        self.ws = torch.empty(self.wsb, dtype=torch.uint8, device=q.device)
+        self.dpair = None if pair is None else torch.empty_like(pair)
+        self.wsb = int(self.L.onionop_flash_attn_bwd_workspace(self.dt, *self.dims))
+        self.ws = torch.empty(max(self.wsb, 1), dtype=torch.uint8, device=q.device)
         self.stream = torch.cuda.current_stream().cuda_stream
         self.chk = _lib.check
 
     def fwd(self):
         p = self.ptr
-        self.chk(self.L.onionop_flash_attn_fwd(self.stream, 2, *self.dims, p(self.q), p(self.k), p(self.v), None,
-                                               None, self.causal, self.scale, p(self.o), p(self.ms), p(self.ls)))
+        self.chk(self.L.onionop_flash_attn_fwd(self.stream, self.dt, *self.dims, p(self.q), p(self.k), p(self.v),
+                                               p(self.pair), p(self.kpad), self.causal, self.scale, p(self.o),
+                                               p(self.ms), p(self.ls)))
 
     def pre(self):
         p = self.ptr
         E, QL, KL, QH, KH, B = self.dims
-        self.chk(self.L.onionop_flash_attn_bwd_preprocess(self.stream, 2, E, QL, QH, B, p(self.do), p(self.o),
+        self.chk(self.L.onionop_flash_attn_bwd_preprocess(self.stream, self.dt, E, QL, QH, B, p(self.do), p(self.o),
                                                           p(self.ms), p(self.ls), p(self.ws), self.wsb))
 
     def dkdv(self):
         p = self.ptr
-        self.chk(self.L.onionop_flash_attn_bwd_dkdv(self.stream, 2, *self.dims, p(self.do), p(self.q), p(self.k),
-                                                    p(self.v), None, None, self.causal, self.scale, 0, p(self.dk),
-                                                    p(self.dv), p(self.ws), self.wsb))
+        self.chk(self.L.onionop_flash_attn_bwd_dkdv(self.stream, self.dt, *self.dims, p(self.do), p(self.q),
+                                                    p(self.k), p(self.v), p(self.pair), p(self.kpad), self.causal,
+                                                    self.scale, self.qk16, p(self.dk), p(self.dv), p(self.ws),
+                                                    self.wsb))
 
     def dq_(self):
         p = self.ptr
-        self.chk(self.L.onionop_flash_attn_bwd_dq(self.stream, 2, *self.dims, p(self.do), p(self.q), p(self.k),
-                                                  p(self.v), None, None, self.causal, self.scale, 0, p(self.dq),
-                                                  None, p(self.ws), self.wsb))
+        self.chk(self.L.onionop_flash_attn_bwd_dq(self.stream, self.dt, *self.dims, p(self.do), p(self.q), p(self.k),
+                                                  p(self.v), p(self.pair), p(self.kpad), self.causal, self.scale,
+                                                  self.qk16, p(self.dq), p(self.dpair), p(self.ws), self.wsb))
 
     def bwd(self):
         """The combined backward (the entry point the drop-in's rrule calls): dQ with the
         preprocess fused, then dK/dV."""
         p = self.ptr
-        self.chk(self.L.onionop_flash_attn_bwd(self.stream, 2, *self.dims, p(self.do), p(self.o), p(self.ms),
-                                               p(self.ls), p(self.q), p(self.k), p(self.v), None, None, self.causal,
-                                               self.scale, 0, p(self.dq), p(self.dk), p(self.dv), None, p(self.ws),
-                                               self.wsb))
+        self.chk(self.L.onionop_flash_attn_bwd(self.stream, self.dt, *self.dims, p(self.do), p(self.o), p(self.ms),
+                                               p(self.ls), p(self.q), p(self.k), p(self.v), p(self.pair),
+                                               p(self.kpad), self.causal, self.scale, self.qk16, p(self.dq),
+                                               p(self.dk), p(self.dv), p(self.dpair), p(self.ws), self.wsb))
 
     def step(self):
         self.fwd()
         self.bwd()
+
+
+class VarlenStep:
+    """One packed variable-length fwd+bwd step through the C ABI (buffers allocated once):
+    q (QH, Tq, E), k / v (KH, Tk, E), sequences at the int32 offsets cu."""
+
+    def __init__(self, torch, nnop, q, k, v, do, cu, max_len, causal=True):
+        from nnop import _lib
+        from nnop._util import dtype_code, ptr
+
+        self.L, self.ptr, self.chk = _lib.lib(), ptr, _lib.check
+        self.q, self.k, self.v, self.do, self.cu = q, k, v, do, cu
+        QH, Tq, E = q.shape
+        KH, Tk, _ = k.shape
+        self.dt = dtype_code(q, "bench")
+        self.dims = (E, Tq, Tk, QH, KH, cu.shape[0] - 1)
+        self.max_len, self.causal = int(max_len), int(causal)
+        self.scale = nnop.attention_scale(E, q.dtype)
+        self.o = torch.zeros_like(q)
+        self.ms = torch.zeros((QH, Tq), dtype=torch.float32, device=q.device)
+        self.ls = torch.zeros_like(self.ms)
+        self.dq, self.dk, self.dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+        self.wsb = int(self.L.onionop_flash_attn_varlen_bwd_workspace(self.dt, E, Tq, QH))
+        self.ws = torch.empty(max(self.wsb, 1), dtype=torch.uint8, device=q.device)
+        self.stream = torch.cuda.current_stream().cuda_stream
+
+    def step(self):
+        p, m = self.ptr, self.max_len
+        self.chk(self.L.onionop_flash_attn_varlen_fwd(self.stream, self.dt, *self.dims, p(self.cu), p(self.cu), m, m,
+                                                      p(self.q), p(self.k), p(self.v), self.causal, self.scale,
+                                                      p(self.o), p(self.ms), p(self.ls)))
+        self.chk(self.L.onionop_flash_attn_varlen_bwd(self.stream, self.dt, *self.dims, p(self.cu), p(self.cu), m, m,
+                                                      p(self.do), p(self.o), p(self.ms), p(self.ls), p(self.q),
+                                                      p(self.k), p(self.v), self.causal, self.scale, 0, p(self.dq),
+                                                      p(self.dk), p(self.dv), p(self.ws), self.wsb))
 
 
 def time_region(torch, fn, iters):
@@ -117,6 +166,24 @@ def time_region(torch, fn, iters):
     en.record()
     torch.cuda.synchronize()
     return st.elapsed_time(en) / iters
+
+
+def settle(torch, fn, min_ms=100.0, max_ms=500.0, chunk=20):
+    """Run fn() until the GPU has reached its steady clocks, before the counted warmup.
+
+    Under this load the MI355X needs some 30 ms to ramp its clocks (the first 50 steps of
+    the headline workload average ~1.8x the steady step time).  Chunks of `chunk` calls are
+    timed with HIP events for at least min_ms of wall time and until two successive chunks
+    agree within 2%, or for at most max_ms.  Returns (wall ms, calls); both are reported."""
+    t0 = time.perf_counter()
+    calls, prev = 0, None
+    while True:
+        t = time_region(torch, fn, chunk)
+        calls += chunk
+        el = (time.perf_counter() - t0) * 1e3
+        if el >= max_ms or (el >= min_ms and prev is not None and abs(t - prev) <= 0.02 * prev):
+            return el, calls
+        prev = t
 
 
 def stage_times(torch, step, iters):
@@ -246,6 +313,18 @@ def memory_bound(torch, nnop, dev, reps=30):
     return out
 
 
+def host_threads():
+    """Host cores this process may use: OMP_NUM_THREADS when set (the GPU host sets it to
+    this job's CPU share), else every core in the process's affinity mask."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
 def cpu_baseline(E=64, L=4096, H=4, B=4, threads=None):
     """The oracle's float32 restatement of the reference tile algorithm on the host."""
     import numpy as np
@@ -253,7 +332,7 @@ def cpu_baseline(E=64, L=4096, H=4, B=4, threads=None):
     import oracle
 
     if threads is None:
-        threads = min(16, os.cpu_count() or 1)
+        threads = host_threads()
     n = oracle.set_threads(threads)
     rng = np.random.default_rng(2)
     s = 1.0 / math.sqrt(E)
@@ -266,93 +345,134 @@ def cpu_baseline(E=64, L=4096, H=4, B=4, threads=None):
     dt = time.perf_counter() - t0
     flops = 14 * B * H * L * L * E / 2
     return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": n, "kind": "port",
+            "nproc": os.cpu_count(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
             "sample": f"one full fwd+bwd step of the headline workload (E,L,H,B)=({E},{L},{H},{B}) causal, "
                       f"float32 tile algorithm of the reference (gsz 64, Float16 Q/K in the backward), "
                       f"{dt:.1f} s"}
 
 
-def workload_timings(torch, nnop, dev):
-    """Steady-state fwd+bwd times of the three other attention workloads at full size, through
-    the nnop API (0.3 s warm, then HIP events): float32 (64,1024,4,2) non-causal with the
-    Float16 Q/K backward, bf16 pair bias (32,768,8,2), and RoPE + causal GQA (128,8192,32:8,4)
-    with per-sequence lengths in [1024, 8192] as a key mask, plus the RoPE backward.
-    One JSON line each; inputs are not rotated (the 18.9 MB bias can sit in the MALL)."""
+def workloads(torch, nnop, dev):
+    """The other attention workloads at full size, timed through the C ABI with buffers
+    allocated once (settled clocks, then HIP events on the library's stream):
+      f32     flash attention f32 (64,1024,4,2) non-causal, q,k,v ~ U[0,1), dO = 1, with the
+              reference's Float16 Q/K backward (default) and with exact float32 Q/K;
+      pair    bf16 (32,768,8,2) non-causal with a pair bias (8,768,768,2), gradients incl. the
+              bias: FLOP rate and algorithmic HBM rate (inputs not rotated: the 18.9 MB bias
+              can sit in the 256 MB MALL);
+      gqa     llama_rope + causal GQA flash attention bf16 (128,8192,32:8,4) with per-sequence
+              lengths U[1024,8192] (seed 4) as a key-padding mask + llama_rope backward, and the
+              same sequences packed (variable-length entry points, RoPE positions per sequence).
+    Rates of the GQA lines count valid work only (7 QH E sum(len^2))."""
     import numpy as np
+    from nnop import _lib
+    from nnop._util import ptr
 
-    def steady(f, iters):
-        t0 = time.time()
-        while time.time() - t0 < 0.3:
-            f()
-        torch.cuda.synchronize()
-        return time_region(torch, f, iters) * 1e3  # us
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(0)
 
-    g = torch.Generator(device="cpu").manual_seed(0)
-    E, L, H, B = 64, 1024, 4, 2
-    q, k, v = [torch.rand((B, H, L, E), generator=g).to(dev) for _ in range(3)]
+    def timed(fn, iters):
+        settle(torch, fn, min_ms=60.0, max_ms=300.0, chunk=max(1, iters // 2))
+        return time_region(torch, fn, iters) * 1e3  # us
+
+    E, QL, H, B = 64, 1024, 4, 2
+    q, k, v = [torch.rand((B, H, QL, E), generator=g, device=dev) for _ in range(3)]
     do = torch.ones_like(q)
+    fl = 14 * B * H * QL * QL * E
+    for qk16 in (1, 0):
+        st = AttnStep(torch, nnop, q, k, v, do, causal=False, qk16=qk16)
+        t = timed(st.step, 50)
+        key = "f32_64x1024x4x2" + ("_qk16" if qk16 else "_exact")
+        out[key] = {"us": round(t, 1), "TFLOP/s": round(fl / t / 1e6, 1),
+                    "frac_of_fp32_mfma": round(fl / t / 1e6 / MI355X_FP32_MFMA_TFLOPS, 3)}
+        log(f"  {key}: {t:.1f} us  {fl / t / 1e6:.1f} TFLOP/s")
+        del st
+    del q, k, v, do
 
-    def f32_step():
-        o, ms, ls = nnop._flash_attention(q, k, v, causal=False)
-        nnop.grad_flash_attention(do, o, ms, ls, q, k, v, causal=False, qk_fp16=True)
+    E, QL, H, B = 32, 768, 8, 2
+    q, k, v, do = [torch.randn((B, H, QL, E), generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    pair = torch.randn((B, QL, QL, H), generator=g, device=dev).to(torch.bfloat16)
+    st = AttnStep(torch, nnop, q, k, v, do, causal=False, pair=pair)
+    t = timed(st.step, 100)
+    fl = 14 * B * H * QL * QL * E
+    # bias read by the forward, dQ and dK/dV, dpair written; q,k,v,o,dO,dq,dk,dv once, o re-read
+    byt = 4 * pair.numel() * 2 + 9 * q.numel() * 2
+    out["pair_bf16_32x768x8x2"] = {"us": round(t, 1), "TFLOP/s": round(fl / t / 1e6, 1),
+                                   "GB/s": round(byt / t / 1e3, 1), "algorithmic_bytes": byt,
+                                   "frac_of_hbm": round(byt / t / 1e3 / MI355X_HBM_GBS, 3),
+                                   "frac_of_bf16_mfma": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 4)}
+    log(f"  pair_bf16_32x768x8x2: {t:.1f} us  {fl / t / 1e6:.1f} TFLOP/s  {byt / t / 1e3:.0f} GB/s")
+    del st, q, k, v, do, pair
 
-    t = steady(f32_step, 50)
-    fl = 14 * B * H * L * L * E
-    print(json.dumps({"workload": "flash_attention fwd+bwd f32 (64,1024,4,2) non-causal, Float16 Q/K backward",
-                      "us": round(t, 1), "TFLOP/s": round(fl / t / 1e6, 1),
-                      "frac_of_fp32_mfma": round(fl / t / 1e6 / MI355X_FP32_MFMA_TFLOPS, 3)}), flush=True)
-
-    E, L, H, B = 32, 768, 8, 2
-    q, k, v, do = [torch.randn((B, H, L, E), generator=g).to(torch.bfloat16).to(dev) for _ in range(4)]
-    pair = torch.randn((B, L, L, H), generator=g).to(torch.bfloat16).to(dev)
-
-    def pair_step():
-        o, ms, ls = nnop._flash_attention(q, k, v, pair, causal=False)
-        nnop.grad_flash_attention(do, o, ms, ls, q, k, v, pair, causal=False)
-
-    t = steady(pair_step, 50)
-    fl = 14 * B * H * L * L * E
-    # bias read by the forward and dK/dV, read and dpair written by dQ; q,k,v,o,dO,dq,dk,dv, o re-read
-    byt = 3 * pair.numel() * 2 + 9 * q.numel() * 2
-    print(json.dumps({"workload": "flash_attention fwd+bwd bf16 (32,768,8,2) non-causal, pair bias, grads incl. bias",
-                      "us": round(t, 1), "TFLOP/s": round(fl / t / 1e6, 1), "GB/s": round(byt / t / 1e3),
-                      "algorithmic_MB": round(byt / 1e6, 1)}), flush=True)
-
-    B, QH, KH, L, E = 4, 32, 8, 8192, 128
-    lens = np.random.default_rng(4).integers(1024, L + 1, size=B)
-    q = torch.randn((B, QH, L, E), generator=g).to(torch.bfloat16).to(dev)
-    k = torch.randn((B, KH, L, E), generator=g).to(torch.bfloat16).to(dev)
-    v = torch.randn((B, KH, L, E), generator=g).to(torch.bfloat16).to(dev)
-    cos, sin = nnop.LlamaRotaryEmbedding(E)(torch.arange(L, dtype=torch.float32)[None].expand(B, L))
+    B, QH, KH, QL, E = 4, 32, 8, 8192, 128
+    lens = np.random.default_rng(4).integers(1024, QL + 1, size=B)
+    fl = 7 * QH * E * sum(int(n) ** 2 for n in lens)
+    rope = nnop.LlamaRotaryEmbedding(E)
+    cos, sin = rope(torch.arange(QL, dtype=torch.float32)[None].expand(B, QL))
     cos, sin = cos.to(dev), sin.to(dev)
-    kp = torch.from_numpy(np.arange(L)[None, :] < lens[:, None]).to(dev)
-    do = torch.randn_like(q) * kp[:, None, :, None]
+    q = torch.randn((B, QH, QL, E), generator=g, device=dev).to(torch.bfloat16)
+    k, v = [torch.randn((B, KH, QL, E), generator=g, device=dev).to(torch.bfloat16) for _ in range(2)]
+    kp = torch.from_numpy(np.arange(QL)[None, :] < lens[:, None]).to(dev)
+    do = (torch.randn((B, QH, QL, E), generator=g, device=dev) * kp[:, None, :, None]).to(torch.bfloat16)
+    qr, kr = torch.empty_like(q), torch.empty_like(k)
+    st = AttnStep(torch, nnop, qr, kr, v, do, causal=True, kpad=kp)
+    dqr, dkr = torch.empty_like(q), torch.empty_like(k)
 
     def gqa_step():
-        qr, kr = nnop._llama_rope(q, k, cos, sin, bwd=False)
-        o, ms, ls = nnop._flash_attention(qr, kr, v, causal=True, kpad_mask=kp)
-        dq, dk, dv, _ = nnop.grad_flash_attention(do, o, ms, ls, qr, kr, v, causal=True, kpad_mask=kp)
-        nnop._llama_rope(dq, dk, cos, sin, bwd=True)
+        _lib.check(L.onionop_llama_rope(stream, 2, E, QL, QH, KH, B, ptr(q), ptr(k), ptr(cos), ptr(sin), 1.0,
+                                        ptr(qr), ptr(kr)))
+        st.step()
+        _lib.check(L.onionop_llama_rope(stream, 2, E, QL, QH, KH, B, ptr(st.dq), ptr(st.dk), ptr(cos), ptr(sin),
+                                        -1.0, ptr(dqr), ptr(dkr)))
 
-    t = steady(gqa_step, 5)
-    fl = 7 * QH * E * sum(int(n) ** 2 for n in lens)  # causal fwd+bwd over each sequence's valid keys
-    print(json.dumps({"workload": "llama_rope + flash_attention fwd+bwd bf16 (128,8192,32:8,4) causal GQA, "
-                      "key mask from per-sequence lengths, + llama_rope bwd", "lens": lens.tolist(),
-                      "us": round(t), "TFLOP/s_valid_work": round(fl / t / 1e6),
-                      "frac_of_bf16_peak": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 3)}), flush=True)
+    t = timed(gqa_step, 6)
+    out["gqa_rope_bf16_128x8192x32:8x4_keymask"] = {
+        "lens": lens.tolist(), "us": round(t), "TFLOP/s_valid_work": round(fl / t / 1e6, 1),
+        "frac_of_bf16_mfma": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 4)}
+    log(f"  gqa keymask: {t:.0f} us  {fl / t / 1e6:.0f} TFLOP/s (valid work)")
+    del st, qr, kr, dqr, dkr
+
+    # the same sequences packed: (QH, sum(len), E); RoPE positions restart per sequence
+    pk = lambda x: torch.cat([x[b, :, :int(n)] for b, n in enumerate(lens)], dim=1).contiguous()
+    qp, kpk, vp, dop = pk(q), pk(k), pk(v), pk(do)
+    del q, k, v, do, kp
+    Tq = int(sum(lens))
+    pos = torch.cat([torch.arange(int(n), dtype=torch.float32) for n in lens])[None]
+    cosp, sinp = [c.to(dev).contiguous() for c in rope(pos)]
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).to(dev)
+    qrp, krp = torch.empty_like(qp), torch.empty_like(kpk)
+    vst = VarlenStep(torch, nnop, qrp, krp, vp, dop, cu, int(max(lens)), causal=True)
+    dqp, dkp = torch.empty_like(qp), torch.empty_like(kpk)
+
+    def packed_step():
+        _lib.check(L.onionop_llama_rope(stream, 2, E, Tq, QH, KH, 1, ptr(qp), ptr(kpk), ptr(cosp), ptr(sinp), 1.0,
+                                        ptr(qrp), ptr(krp)))
+        vst.step()
+        _lib.check(L.onionop_llama_rope(stream, 2, E, Tq, QH, KH, 1, ptr(vst.dq), ptr(vst.dk), ptr(cosp),
+                                        ptr(sinp), -1.0, ptr(dqp), ptr(dkp)))
+
+    t = timed(packed_step, 6)
+    out["gqa_rope_bf16_128x8192x32:8x4_packed"] = {
+        "lens": lens.tolist(), "us": round(t), "TFLOP/s_valid_work": round(fl / t / 1e6, 1),
+        "frac_of_bf16_mfma": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 4)}
+    log(f"  gqa packed: {t:.0f} us  {fl / t / 1e6:.0f} TFLOP/s (valid work)")
+    return out
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    # The GPU reaches its steady clocks only after some 30 ms of this load (the first 50
-    # steps average ~1.8x the steady step time), so the default warmup is 200 steps (~40 ms).
-    ap.add_argument("--warmup", type=int, default=200)
+    # Counted warmup steps; before them a settle phase (reported as settle_ms / settle_steps)
+    # runs the step until the GPU's clocks are steady (see settle()).
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-memory", action="store_true", help="skip the HBM-bound kernel set")
+    ap.add_argument("--no-workloads", action="store_true", help="skip the other attention workloads")
     ap.add_argument("--workloads", action="store_true",
-                    help="instead of the bench line, time the other attention workloads (float32, "
-                         "pair bias, RoPE + GQA) and print one JSON line each")
+                    help="only time the other attention workloads (float32, pair bias, RoPE + GQA key mask "
+                         "and packed) and print them as one JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run 3 plain device copies of MIB MiB (a known-size kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -367,12 +487,14 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.workloads:
-        workload_timings(torch, nnop, dev)
+        print(json.dumps(workloads(torch, nnop, dev)), flush=True)
         return
     E, L, H, B = 64, 4096, 4, 4
     q, k, v, do = attention_setup(torch, nnop, dev, E, L, H, B)
     step = AttnStep(torch, nnop, q, k, v, do, causal=True)
-    log(f"bench: flash attention fwd+bwd bf16 (E,L,H,B)=({E},{L},{H},{B}) causal; warmup {args.warmup}")
+    settle_ms, settle_steps = settle(torch, step.step)
+    log(f"bench: flash attention fwd+bwd bf16 (E,L,H,B)=({E},{L},{H},{B}) causal; settled clocks in "
+        f"{settle_ms:.0f} ms ({settle_steps} steps); warmup {args.warmup}")
     for _ in range(args.warmup):
         step.step()
     torch.cuda.synchronize()
@@ -394,7 +516,8 @@ def main():
 
     result = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "settle_ms": round(settle_ms, 1), "settle_steps": settle_steps,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1)/sqrt(E) q,k,v; dO = 1)",
         "config": {"workload": "flash_attention fwd+bwd bf16 (E,L,H,B)=(64,4096,4,4) causal",
                    "E": E, "L": L, "H": H, "B": B, "causal": True, "flops_per_step": flops,
@@ -413,6 +536,10 @@ def main():
     if not args.no_memory:
         log("bench: HBM-bound kernels")
         result["memory_bound"] = memory_bound(torch, nnop, dev)
+    if not args.no_workloads:
+        log("bench: other attention workloads")
+        del q, k, v, do, step
+        result["workloads"] = workloads(torch, nnop, dev)
     if not args.no_cpu:
         log("bench: CPU baseline (oracle port, float32)")
         result["cpu_baseline"] = cpu_baseline(E, L, H, B)

@@ -23,6 +23,13 @@
  *    of the last error of the calling thread is returned by onionop_last_error().
  *    Shape errors carry the reference's own messages.
  *  - All pointers are device pointers, except where stated.
+ *  - Alignment: q, k, v, o, dO, dq, dk, dv, x, y, dx, dy, g and the RoPE in/outputs must
+ *    be 16-byte aligned (the kernels use 16-byte vector accesses); a misaligned pointer
+ *    returns ONIONOP_E_SHAPE before anything is enqueued.  Allocations are; a view that
+ *    starts inside its allocation (a Julia `view`, an offset pointer) may not be, and the
+ *    binding copies such an array into a fresh one first.  Weights, biases, statistics,
+ *    the pair bias and the key mask have no alignment requirement (the four-head bias
+ *    path is only taken when pair / dpair are 8-byte aligned).
  */
 #ifndef ONIONOP_H
 #define ONIONOP_H
@@ -186,6 +193,10 @@ int onionop_flash_attn_varlen_bwd(void* stream, int dtype,
  * Online softmax over dim 1 of x (N, M): y[:, j] = exp(x[:, j] - max) / sum.
  * Replaces `online_softmax` (src/softmax.jl:60-68) and its kernel
  * `online_softmax!` (src/softmax.jl:19-58).  Computed in float32; y has x's dtype.
+ * Any N up to 2^29 - 1: rows a workgroup's registers cannot hold (N > 16384 float32 /
+ * 32768 16-bit, or N > 4096 when N * sizeof(T) is not a multiple of 16) are streamed with
+ * the online (max, sum) merge of the reference's md_reduce (src/softmax.jl:1-16,204-253).
+ * The same row-length rule holds for the softmax backward and the norms below.
  */
 int onionop_softmax_fwd(void* stream, int dtype, int64_t N, int64_t M,
                         const void* x, void* y);

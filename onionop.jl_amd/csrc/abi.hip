@@ -301,8 +301,7 @@ int onionop_flash_attn_varlen_bwd(void* stream, int dtype, int64_t E, int64_t Tq
 static int check_rows(const char* what, int dtype, int64_t n, int64_t rows) {
     if (!valid_dt(dtype)) return fail(ONIONOP_E_DTYPE, "%s: unsupported element type code %d", what, dtype);
     if (n < 0 || rows < 0) return fail(ONIONOP_E_SHAPE, "%s: negative dimension", what);
-    const int64_t vec = 16 / (int64_t)dt_size(dtype);
-    const int64_t lim = (n % vec == 0) ? onionop::max_row_elems(dtype) : 16 * 256;
+    const int64_t lim = onionop::max_row_elems(dtype);
     if (n > lim)
         return fail(ONIONOP_E_UNSUPPORTED, "%s: reduction length %lld exceeds the supported %lld", what,
                     (long long)n, (long long)lim);

@@ -31,11 +31,13 @@ struct RowIO {
     static __device__ __forceinline__ uint32_t off(int i) {
         return (uint32_t)(VEC * (threadIdx.x + i * kThreads)) * (uint32_t)sizeof(T);
     }
-    static __device__ __forceinline__ raw load(rsrc_t r, int i) {
-        if constexpr (VEC != 1) return bload16_nt(r, off(i));
-        else if constexpr (sizeof(T) == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off(i), 0, kNT);
-        else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off(i), 0, kNT);
+    // the slot at byte offset o of the resource
+    static __device__ __forceinline__ raw load_at(rsrc_t r, uint32_t o) {
+        if constexpr (VEC != 1) return bload16_nt(r, o);
+        else if constexpr (sizeof(T) == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, (int)o, 0, kNT);
+        else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)o, 0, kNT);
     }
+    static __device__ __forceinline__ raw load(rsrc_t r, int i) { return load_at(r, off(i)); }
     static __device__ __forceinline__ void to_float(raw v, float* out) {
         if constexpr (VEC != 1) {
             union { u32x4 v; T e[VEC]; } u;
@@ -50,20 +52,21 @@ struct RowIO {
             out[0] = to_f32(u.e);
         }
     }
-    static __device__ __forceinline__ void store(rsrc_t r, int i, const float* in) {
+    static __device__ __forceinline__ void store_at(rsrc_t r, uint32_t o, const float* in) {
         if constexpr (VEC != 1) {
             union { u32x4 v; T e[VEC]; } u;
 #pragma unroll
             for (int j = 0; j < VEC; ++j) u.e[j] = from_f32<T>(in[j]);
-            bstore16_nt(u.v, r, off(i));
+            bstore16_nt(u.v, r, o);
         } else if constexpr (sizeof(T) == 4) {
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(in[0]), r, (int)off(i), 0, kNT);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(in[0]), r, (int)o, 0, kNT);
         } else {
             union { uint16_t s; T e; } u;
             u.e = from_f32<T>(in[0]);
-            __builtin_amdgcn_raw_buffer_store_b16(u.s, r, (int)off(i), 0, kNT);
+            __builtin_amdgcn_raw_buffer_store_b16(u.s, r, (int)o, 0, kNT);
         }
     }
+    static __device__ __forceinline__ void store(rsrc_t r, int i, const float* in) { store_at(r, off(i), in); }
 };
 
 // Resource over row r of a (rows x n) matrix; an empty one for r >= rows (its loads
@@ -684,6 +687,8 @@ __global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ 
     else reinterpret_cast<bf16*>(out)[e] = from_f32<bf16>(s);
 }
 
+#include "rowwise_long.inc"
+
 // ------------------------------------------------------------------ dispatch
 
 // Row blocks in flight ahead of the one being computed by the norm backward: two while
@@ -830,6 +835,88 @@ struct LnBwd {
     }
 };
 
+// Rows the register-resident kernels cannot hold: the streaming kernels of
+// rowwise_long.inc, 16-byte vectors when rows stay 16-byte aligned, else scalars.
+template <typename T, template <typename, int> class K, typename... Args>
+static bool dispatch_long(int64_t n, Args&&... args) {
+    if (n % Vec<T>::N == 0) return K<T, Vec<T>::N>::run(args...);
+    return K<T, 1>::run(args...);
+}
+
+// Persistent grid of a streaming kernel: up to 8 workgroups per CU (no more than fit).
+template <typename Kern>
+static unsigned grid_long(Kern k, int64_t rows) {
+    int fit = fit_per_cu(k);
+    fit = fit > 8 ? 8 : fit;
+    const int64_t g = (int64_t)fit * num_cus();
+    return (unsigned)(rows < g ? rows : g);
+}
+
+template <typename T, int VEC>
+struct SoftmaxFwdLong {
+    static bool run(hipStream_t s, const void* x, void* y, int64_t n, int64_t rows) {
+        const auto k = softmax_fwd_long_kernel<T, VEC>;
+        k<<<dim3(grid_long(k, rows)), dim3(kThreads), 0, s>>>((const T*)x, (T*)y, n, rows);
+        return true;
+    }
+};
+template <typename T, int VEC>
+struct SoftmaxBwdLong {
+    static bool run(hipStream_t s, const void* dy, const void* y, void* dx, int64_t n, int64_t rows) {
+        const auto k = softmax_bwd_long_kernel<T, VEC>;
+        k<<<dim3(grid_long(k, rows)), dim3(kThreads), 0, s>>>((const T*)dy, (const T*)y, (T*)dx, n, rows);
+        return true;
+    }
+};
+template <typename T, int VEC>
+struct SoftmaxBwd2Long {
+    static bool run(hipStream_t s, const void* g, const void* dy, const void* y, void* d_dy, void* d_y, int64_t n,
+                    int64_t rows) {
+        const auto k = softmax_bwd2_long_kernel<T, VEC>;
+        k<<<dim3(grid_long(k, rows)), dim3(kThreads), 0, s>>>((const T*)g, (const T*)dy, (const T*)y, (T*)d_dy,
+                                                              (T*)d_y, n, rows);
+        return true;
+    }
+};
+template <typename T, int VEC>
+struct RmsFwdLong {
+    static bool run(hipStream_t s, const void* x, const void* w, int dtw, void* y, float* rstd, int64_t n,
+                    int64_t rows, float eps, float offset) {
+        const auto k = rms_fwd_long_kernel<T, VEC>;
+        k<<<dim3(grid_long(k, rows)), dim3(kThreads), 0, s>>>((const T*)x, w, dtw, (T*)y, rstd, n, rows, eps,
+                                                              offset);
+        return true;
+    }
+};
+template <typename T, int VEC>
+struct RmsBwdLong {
+    static bool run(hipStream_t s, const void* dy, const float* rstd, const void* x, const void* w, int dtw,
+                    float offset, void* dx, float* ws, int64_t groups, int64_t n, int64_t rows) {
+        rms_bwd_long_kernel<T, VEC><<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>(
+            (const T*)dy, rstd, (const T*)x, w, dtw, offset, (T*)dx, ws, n, rows);
+        return true;
+    }
+};
+template <typename T, int VEC>
+struct LnFwdLong {
+    static bool run(hipStream_t s, const void* x, const void* w, const void* b, int dtw, void* y, float* mu,
+                    float* rstd, int64_t n, int64_t rows, float eps) {
+        const auto k = ln_fwd_long_kernel<T, VEC>;
+        k<<<dim3(grid_long(k, rows)), dim3(kThreads), 0, s>>>((const T*)x, w, b, dtw, (T*)y, mu, rstd, n, rows,
+                                                              eps);
+        return true;
+    }
+};
+template <typename T, int VEC>
+struct LnBwdLong {
+    static bool run(hipStream_t s, const void* dy, const float* mu, const float* rstd, const void* x,
+                    const void* w, int dtw, void* dx, float* ws, int64_t groups, int64_t n, int64_t rows) {
+        ln_bwd_long_kernel<T, VEC><<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>(
+            (const T*)dy, mu, rstd, (const T*)x, w, dtw, (T*)dx, ws, n, rows);
+        return true;
+    }
+};
+
 #define ONIONOP_DT_SWITCH(dt, T, ...)                    \
     switch (dt) {                                        \
         case 0: { typedef float T; __VA_ARGS__; } break; \
@@ -838,9 +925,11 @@ struct LnBwd {
         default: return false;                           \
     }
 
+// Longest row: the kernels address a row (and a partial row of the norm backward) with
+// 32-bit byte offsets.
 int64_t max_row_elems(int dt) {
-    const int es = dt == 0 ? 4 : 2;
-    return 16LL * kThreads * (16 / es);
+    (void)dt;
+    return (1LL << 29) - 1;
 }
 
 // Partial-row groups (= workgroups) of the norm backward for rows of n elements.  A
@@ -866,24 +955,28 @@ static void colsum(hipStream_t s, float* ws, int64_t groups, int64_t n, int coun
 
 bool launch_softmax_fwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* x, void* y) {
     if (rows == 0 || n == 0) return true;
-    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, SoftmaxFwd>(n, s, x, y, n, rows));
+    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, SoftmaxFwd>(n, s, x, y, n, rows) ||
+                                    dispatch_long<T, SoftmaxFwdLong>(n, s, x, y, n, rows));
     return true;
 }
 bool launch_softmax_bwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* dy, const void* y, void* dx) {
     if (rows == 0 || n == 0) return true;
-    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, SoftmaxBwd>(n, s, dy, y, dx, n, rows));
+    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, SoftmaxBwd>(n, s, dy, y, dx, n, rows) ||
+                                    dispatch_long<T, SoftmaxBwdLong>(n, s, dy, y, dx, n, rows));
     return true;
 }
 bool launch_softmax_bwd_bwd(hipStream_t s, int dt, int64_t n, int64_t rows, const void* g, const void* dy,
                             const void* y, void* d_dy, void* d_y) {
     if (rows == 0 || n == 0) return true;
-    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, SoftmaxBwd2>(n, s, g, dy, y, d_dy, d_y, n, rows));
+    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, SoftmaxBwd2>(n, s, g, dy, y, d_dy, d_y, n, rows) ||
+                                    dispatch_long<T, SoftmaxBwd2Long>(n, s, g, dy, y, d_dy, d_y, n, rows));
     return true;
 }
 bool launch_rms_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* x, const void* w,
                     float eps, float offset, void* y, float* rstd) {
     if (rows == 0) return true;
-    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, RmsFwd>(n, s, x, w, dtw, y, rstd, n, rows, eps, offset));
+    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, RmsFwd>(n, s, x, w, dtw, y, rstd, n, rows, eps, offset) ||
+                                    dispatch_long<T, RmsFwdLong>(n, s, x, w, dtw, y, rstd, n, rows, eps, offset));
     return true;
 }
 bool launch_rms_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* dy, const float* rstd,
@@ -892,7 +985,9 @@ bool launch_rms_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, con
     if (rows > 0) {
         bool ok = false;
         ONIONOP_DT_SWITCH(dt, T,
-                          ok = dispatch_row<T, RmsBwd>(n, s, dy, rstd, x, w, dtw, offset, dx, ws, groups, n, rows));
+                          ok = dispatch_row<T, RmsBwd>(n, s, dy, rstd, x, w, dtw, offset, dx, ws, groups, n, rows) ||
+                               dispatch_long<T, RmsBwdLong>(n, s, dy, rstd, x, w, dtw, offset, dx, ws, groups, n,
+                                                            rows));
         if (!ok) return false;
     }
     if (n == 0) return true;
@@ -906,7 +1001,8 @@ bool launch_rms_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, con
 bool launch_ln_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* x, const void* w,
                    const void* b, float eps, void* y, float* mu, float* rstd) {
     if (rows == 0) return true;
-    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, LnFwd>(n, s, x, w, b, dtw, y, mu, rstd, n, rows, eps));
+    ONIONOP_DT_SWITCH(dt, T, return dispatch_row<T, LnFwd>(n, s, x, w, b, dtw, y, mu, rstd, n, rows, eps) ||
+                                    dispatch_long<T, LnFwdLong>(n, s, x, w, b, dtw, y, mu, rstd, n, rows, eps));
     return true;
 }
 bool launch_ln_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* dy, const float* mu,
@@ -920,7 +1016,9 @@ bool launch_ln_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, cons
         return true;
     }
     bool ok = false;
-    ONIONOP_DT_SWITCH(dt, T, ok = dispatch_row<T, LnBwd>(n, s, dy, mu, rstd, x, w, dtw, dx, ws, groups, n, rows));
+    ONIONOP_DT_SWITCH(dt, T, ok = dispatch_row<T, LnBwd>(n, s, dy, mu, rstd, x, w, dtw, dx, ws, groups, n, rows) ||
+                                  dispatch_long<T, LnBwdLong>(n, s, dy, mu, rstd, x, w, dtw, dx, ws, groups, n,
+                                                              rows));
     if (!ok) return false;
     colsum(s, ws, groups, n, 2, dw, db, dtw);
     return true;

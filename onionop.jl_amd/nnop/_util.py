@@ -16,12 +16,19 @@ def dtype_code(t: torch.Tensor, what: str) -> int:
 
 
 def device_tensor(t: torch.Tensor, what: str) -> torch.Tensor:
-    """Dense device tensor (the reference's dense arrays); no host fallback exists."""
+    """Dense, 16-byte aligned device tensor (the reference's dense arrays); no host fallback
+    exists.  The library's kernels use 16-byte vector accesses and reject pointers that are
+    not 16-byte aligned; a view that starts inside its storage (a slice of a larger array,
+    the counterpart of a Julia `view`) is copied into a fresh allocation here, as the Julia
+    binding does for misaligned arrays."""
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{what}: expected a torch.Tensor, got {type(t).__name__}")
     if t.device.type != "cuda":
         raise ValueError(f"{what}: tensor must be on a ROCm device (got {t.device}); there is no CPU path")
-    return t.contiguous()
+    t = t.contiguous()
+    if t.data_ptr() % 16 != 0:
+        t = t.clone()
+    return t
 
 
 def ptr(t):

@@ -174,9 +174,11 @@ def _flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: i
     q, k, v = (device_tensor(t, "flash_attention (varlen)") for t in (q, k, v))
     QH, Tq, E, KH, Tk, B = _check_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k)
     dt = dtype_code(q, "flash_attention (varlen)")
-    o = torch.empty_like(q)
-    ms = torch.empty((QH, Tq), dtype=torch.float32, device=q.device)
-    ls = torch.empty((QH, Tq), dtype=torch.float32, device=q.device)
+    # Rows in no sequence (a packing buffer's tail, rows past max_seqlen_q) are not
+    # written by the kernels: they start at zero (ls = 0 marks them as empty rows).
+    o = torch.zeros_like(q)
+    ms = torch.zeros((QH, Tq), dtype=torch.float32, device=q.device)
+    ls = torch.zeros((QH, Tq), dtype=torch.float32, device=q.device)
     _lib.check(_lib.lib().onionop_flash_attn_varlen_fwd(
         stream_of(q), dt, E, Tq, Tk, QH, KH, B, ptr(cu_seqlens_q), ptr(cu_seqlens_k), int(max_seqlen_q),
         int(max_seqlen_k), ptr(q), ptr(k), ptr(v), int(bool(causal)), attention_scale(E, q.dtype), ptr(o), ptr(ms),
@@ -196,7 +198,8 @@ def grad_flash_attention_varlen(do, o, ms, ls, q, k, v, cu_seqlens_q, cu_seqlens
     L = _lib.lib()
     ws_bytes = L.onionop_flash_attn_varlen_bwd_workspace(dt, E, Tq, QH)
     ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    # Gradient rows of queries / keys in no sequence are not written: they are zero.
+    dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
     _lib.check(L.onionop_flash_attn_varlen_bwd(
         stream_of(q), dt, E, Tq, Tk, QH, KH, B, ptr(cu_seqlens_q), ptr(cu_seqlens_k), int(max_seqlen_q),
         int(max_seqlen_k), ptr(do), ptr(o), ptr(ms), ptr(ls), ptr(q), ptr(k), ptr(v), int(bool(causal)),

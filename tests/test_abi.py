@@ -80,7 +80,11 @@ def test_c_abi_validation_errors():
     assert st == -3 and b"pair bias too large" in L.onionop_last_error()
     st = L.onionop_llama_rope(None, 2, 15, 4, 1, 1, 1, 16, 16, 16, 16, 1.0, 16, 16)
     assert st == -1
-    st = L.onionop_softmax_fwd(None, 0, 1 << 20, 4, 16, 16)
+    # rows of any length run (streaming kernels past the register-resident size), up to
+    # the 32-bit row offsets
+    st = L.onionop_softmax_fwd(None, 0, 1 << 29, 4, 16, 16)
+    assert st == -3 and b"reduction length" in L.onionop_last_error()
+    st = L.onionop_rms_norm_fwd(None, 2, 2, 1 << 29, 4, 16, 16, 1e-6, 0.0, 16, 16)
     assert st == -3
 
 
@@ -109,3 +113,44 @@ def test_no_cpu_fallback():
     q = torch.zeros((1, 2, 8, 64))
     with pytest.raises(ValueError, match="no CPU path"):
         nnop.flash_attention(q, q, q, causal=True)
+
+
+def test_lds_query_errors():
+    """onionop_device_lds_bytes (the shared_memory query, src/NNop.jl:27-30) rejects a NULL
+    output and a device index outside the cache before touching a device."""
+    L = nnop.lib()
+    assert L.onionop_device_lds_bytes(0, None) == -5
+    out = ctypes.c_size_t(7)
+    assert L.onionop_device_lds_bytes(-1, ctypes.byref(out)) == -1
+    assert L.onionop_device_lds_bytes(64, ctypes.byref(out)) == -1
+    assert out.value == 7
+
+
+def test_llama_rotary_embedding_tables():
+    """nnop.LlamaRotaryEmbedding (src/rope/llama_rope.jl:1-22) against the oracle's float32
+    restatement (FAITHFUL) and the float64 closed form cos/sin(p / base^(2i/dim)), for the
+    headline GQA workload's table: dim 128, positions 0..8191, 4 sequences."""
+    import numpy as np
+
+    import oracle
+
+    dim, L, B = 128, 8192, 4
+    pos = torch.arange(L, dtype=torch.float32)[None].expand(B, L)
+    c, s = nnop.LlamaRotaryEmbedding(dim)(pos)
+    assert tuple(c.shape) == (B, L, dim) and c.dtype == torch.float32
+    c, s = c.double().numpy(), s.double().numpy()
+    # first and second halves repeat (vcat(freqs, freqs))
+    assert np.array_equal(c[..., :64], c[..., 64:]) and np.array_equal(s[..., :64], s[..., 64:])
+    cf, sf = oracle.rotary_embedding(dim, pos.double().numpy(), mode=oracle.FAITHFUL)
+    assert np.abs(c - cf).max() <= 2e-7 and np.abs(s - sf).max() <= 2e-7
+    # closed form in float64; the float32 angle p * inv_freq carries up to ~L ulp(1) of
+    # error at the largest positions, which bounds the distance
+    i = np.arange(0, dim, 2) / dim
+    ang = np.arange(L)[:, None] / 10000.0 ** i[None, :]
+    ang = np.concatenate([ang, ang], axis=1)[None]
+    assert np.abs(c - np.cos(ang)).max() <= L * 2.0 ** -23 and np.abs(s - np.sin(ang)).max() <= L * 2.0 ** -23
+    ce, se = oracle.rotary_embedding(dim, pos.double().numpy(), mode=oracle.EXACT)
+    assert np.abs(ce - np.cos(ang)).max() <= 1e-12 and np.abs(se - np.sin(ang)).max() <= 1e-12
+    # positions as a vector give the table of one sequence
+    c1, _ = nnop.LlamaRotaryEmbedding(dim)(torch.arange(L, dtype=torch.float32))
+    assert np.array_equal(c1.double().numpy()[0], c[0])

@@ -240,3 +240,15 @@ def test_staged_backward_matches_combined(dev, dt, E, L, QH, KH, causal, use_pai
         pairs["dpair"] = (dpair, dpair2)
     errs = {n: rel_err(host(a), host(b)) for n, (a, b) in pairs.items()}
     assert all(e <= tol for e in errs.values()), errs
+
+
+def test_shared_memory_query(dev):
+    """NNop.shared_memory (src/NNop.jl:27-30, ext/NNopAMDGPUExt.jl:6-9): the LDS bytes per
+    workgroup of the device, as hipDeviceProp_t.sharedMemPerBlock reports it (torch reads
+    the same property), cached per device."""
+    expect = torch.cuda.get_device_properties(0).shared_memory_per_block
+    got = nnop.shared_memory(0)
+    assert got == expect
+    assert nnop.shared_memory(0) == got  # memoised value
+    # every attention kernel's static LDS fits in it (the largest uses 133120 bytes)
+    assert got >= 133120

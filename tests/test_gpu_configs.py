@@ -46,25 +46,32 @@ def test_config1_f32_attention(dev):
     o_r, _, _ = oracle.attn_fwd(qn, kn, vn, causal=False, scale=scale)
     of, msf, lsf = oracle.attn_fwd(qn, kn, vn, causal=False, scale=scale, mode=oracle.FAITHFUL)
     errs = {"o": rel_err(host(o), o_r)}
-    # With q, k, v ~ U[0,1) and dO = 1, dQ is ill-conditioned: dP - delta cancels ~14x and
-    # dQ = sum_k dS K cancels again on K's mean of 0.5, so any float32 evaluation loses
-    # ~1e-4 against float64 -- the reference's own float32 algorithm (the oracle's
-    # FAITHFUL replay of it) included.  dQ is held to "no worse than that algorithm on the
-    # same inputs"; every other output to 1e-5.  Both the exact float32 backward and the
-    # reference's Float16 Q/K mode are checked against float64 math in the same mode.
-    dq_tol = {}
+    # With q, k, v ~ U[0,1) and dO = 1, dQ = scale sum_k dS K cancels on K's mean of 0.5.
+    # The exact float32 backward centres K (every row of dS sums to zero) and is held to
+    # 1e-5 against float64 like every other output.  In the reference's Float16 Q/K mode the
+    # rows of P do not sum to one (S from rounded Q/K, lse from the float32 forward), so dQ
+    # carries the reference algorithm's own error (~1e-4 against float64): there dQ is held
+    # to "no worse than that algorithm" (the oracle's FAITHFUL replay of it) and its
+    # distance to that replay is printed.
+    extra = {}
     for qk16 in (False, True):
         sfx = "_16" if qk16 else ""
         dq, dk, dv, _ = nnop.grad_flash_attention(do, o, ms, ls, q, k, v, causal=False, qk_fp16=qk16)
         dq_r, dk_r, dv_r, _ = oracle.attn_bwd(np.ones_like(qn), qn, kn, vn, causal=False, scale=scale,
                                               qk_fp16=qk16)
-        dq_f, _, _, _ = oracle.attn_bwd(np.ones_like(qn), qn, kn, vn, causal=False, scale=scale,
-                                        mode=oracle.FAITHFUL, o=of, ms=msf, ls=lsf, qk_fp16=qk16)
-        dq_tol["dq" + sfx] = max(1e-5, rel_err(dq_f, dq_r))
         errs.update({"dk" + sfx: rel_err(host(dk), dk_r), "dv" + sfx: rel_err(host(dv), dv_r)})
+        if not qk16:
+            errs["dq"] = rel_err(host(dq), dq_r)
+            continue
+        dq_f, dk_f, dv_f, _ = oracle.attn_bwd(np.ones_like(qn), qn, kn, vn, causal=False, scale=scale,
+                                              mode=oracle.FAITHFUL, o=of, ms=msf, ls=lsf, qk_fp16=True)
+        bound = max(1e-5, rel_err(dq_f, dq_r))
         dq_err = rel_err(host(dq), dq_r)
-        assert dq_err <= dq_tol["dq" + sfx], (dq_err, dq_tol)
-    print("config 1 errors", errs, "dq bounds (reference float32 algorithm)", dq_tol, flush=True)
+        extra = {"dq_16 vs float64": dq_err, "FAITHFUL dq_16 vs float64": bound,
+                 "dq_16 vs FAITHFUL": rel_err(host(dq), dq_f), "dk_16 vs FAITHFUL": rel_err(host(dk), dk_f),
+                 "dv_16 vs FAITHFUL": rel_err(host(dv), dv_f)}
+        assert dq_err <= bound, (dq_err, bound)
+    print("config 1 errors", errs, "Float16 Q/K mode", extra, flush=True)
     check(errs, 1e-5)
 
 

@@ -136,6 +136,34 @@ def test_varlen_autograd(dev):
         assert rel_err(host(q.grad)[:, s0:s1], dq_r[0]) <= 1e-5
 
 
+def test_varlen_autograd_tail_rows(dev):
+    """A packing buffer longer than its sequences (40 tail rows in no sequence): the
+    output and gradient rows the kernels never visit are exactly zero, in o, q, k and v."""
+    rng = np.random.default_rng(4)
+    QH, KH, E, T = 4, 2, 64, 210
+    cu = torch.tensor([0, 100, 170], dtype=torch.int32, device=dev)
+    q, qn = make(rng, (QH, T, E), torch.bfloat16, dev)
+    k, kn = make(rng, (KH, T, E), torch.bfloat16, dev)
+    v, vn = make(rng, (KH, T, E), torch.bfloat16, dev)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    print("varlen autograd: 40 tail rows, bf16 E=64 4:2 causal", flush=True)
+    o = nnop.flash_attention_varlen(q, k, v, cu, cu, 100, 100, causal=True)
+    o.float().sum().backward()
+    torch.cuda.synchronize()
+    for name, t in (("o", o), ("dq", q.grad), ("dk", k.grad), ("dv", v.grad)):
+        a = host(t)
+        assert np.isfinite(a).all(), name
+        assert (a[:, 170:] == 0).all(), f"{name}: rows in no sequence must be zero"
+    scale = nnop.attention_scale(E, torch.bfloat16)
+    for s0, s1 in ((0, 100), (100, 170)):
+        sl = lambda a: a[:, s0:s1][None]
+        dq_r, dk_r, dv_r, _ = oracle.attn_bwd(np.ones((1, QH, s1 - s0, E)), sl(qn), sl(kn), sl(vn), None, None,
+                                              True, scale)
+        for name, got, ref in (("dq", q.grad, dq_r), ("dk", k.grad, dk_r), ("dv", v.grad, dv_r)):
+            assert rel_err(host(got)[:, s0:s1], ref[0]) <= 2e-2, name
+
+
 def test_varlen_errors(dev):
     q = torch.zeros((2, 10, 64), dtype=torch.bfloat16, device=dev)
     cu = torch.tensor([0, 10], dtype=torch.int32, device=dev)
