@@ -124,6 +124,26 @@ int onionop_flash_attn_bwd(void* stream, int dtype,
                            void* workspace, size_t workspace_bytes);
 
 /*
+ * onionop_flash_attn_bwd without a workspace argument and without any allocation.
+ * No counterpart in the reference: this entry point is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as onionop_flash_attn_bwd; the workspace is a
+ * device array the library owns, 16 MiB on each GPU it runs on, held until the process
+ * ends, so B * QH * QL may be at most 2097120 query rows (8 bytes each); larger calls
+ * return ONIONOP_E_UNSUPPORTED without enqueueing anything.  Every call on one GPU uses
+ * that GPU's array: calls whose kernels overlap on one GPU (on different streams, or from
+ * several threads) race and give wrong results, so serialise them.  Nothing in the array
+ * needs to be zero between calls.
+ */
+int onionop_flash_attn_bwd_noalloc(void* stream, int dtype,
+                                   int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B,
+                                   const void* dO, const void* o, const float* ms, const float* ls,
+                                   const void* q, const void* k, const void* v,
+                                   const void* pair, const uint8_t* kpad,
+                                   int causal, float scale, int qk_fp16,
+                                   void* dq, void* dk, void* dv, void* dpair);
+
+/*
  * The three stages onionop_flash_attn_bwd runs, callable one by one (same arguments,
  * same workspace; call them in this order on one stream).
  *  _preprocess: delta = rowsum(dO .* o) and the log-sum-exp of every query row into the

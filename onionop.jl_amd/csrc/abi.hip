@@ -78,6 +78,40 @@ bool g_lds_set[64];
 
 }  // namespace
 
+// Scratch of onionop_flash_attn_bwd_noalloc: the backward's workspace (per query row, the
+// log2-sum-exp and delta, 8 bytes, written by the dQ kernel before the dK/dV kernel reads
+// them) in a device array the library owns, so that entry point allocates nothing.  Each
+// GPU the library runs on holds its own copy until the process ends.  In host code the
+// array's name is not a device address: the address is looked up once per device with
+// hipGetSymbolAddress and only that pointer is used.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];  // device address of `scratch` on device d, once looked up
+
+// The scratch array's address on the current device (looked up on the first call there).
+int scratch_on_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(ONIONOP_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= 64) return fail(ONIONOP_E_HIP, "device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return fail(ONIONOP_E_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return ONIONOP_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* onionop_last_error(void) { return g_err; }
@@ -186,6 +220,28 @@ int onionop_flash_attn_bwd(void* stream, int dtype, int64_t E, int64_t QL, int64
     return attn_bwd_common("∇flash_attention", onionop::kBwdAll, stream, dtype, E, QL, KL, QH, KH, B, dO, o, ms, ls,
                            q, k, v, pair, kpad, causal, scale, qk_fp16, dq, dk, dv, dpair, workspace,
                            workspace_bytes);
+}
+
+int onionop_flash_attn_bwd_noalloc(void* stream, int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH,
+                                   int64_t KH, int64_t B, const void* dO, const void* o, const float* ms,
+                                   const float* ls, const void* q, const void* k, const void* v, const void* pair,
+                                   const uint8_t* kpad, int causal, float scale, int qk_fp16, void* dq, void* dk,
+                                   void* dv, void* dpair) {
+    const char* what = "∇flash_attention (no allocation)";
+    int st = check_attn(dtype, E, QL, KL, QH, KH, B);
+    if (st) return st;
+    const size_t need = onionop_flash_attn_bwd_workspace(dtype, E, QL, KL, QH, KH, B);
+    if (need > kScratchBytes)
+        return fail(ONIONOP_E_UNSUPPORTED,
+                    "%s: needs %zu bytes of scratch (8 per query row), the library holds %zu "
+                    "(at most %zu query rows B*QH*QL); use onionop_flash_attn_bwd with a workspace",
+                    what, need, kScratchBytes, (kScratchBytes - 256) / 8);
+    void* ws = nullptr;
+    if (need > 0 && (st = scratch_on_current_device(&ws))) return st;
+    // Nothing in the scratch has to start at zero: every value the dK/dV kernel reads is
+    // written first by the dQ kernel of the same call.
+    return attn_bwd_common(what, onionop::kBwdAll, stream, dtype, E, QL, KL, QH, KH, B, dO, o, ms, ls, q, k, v, pair,
+                           kpad, causal, scale, qk_fp16, dq, dk, dv, dpair, ws, need > 0 ? kScratchBytes : 0);
 }
 
 int onionop_flash_attn_bwd_preprocess(void* stream, int dtype, int64_t E, int64_t QL, int64_t QH, int64_t B,

@@ -30,6 +30,8 @@ SIGNATURES = {
     "onionop_flash_attn_bwd_workspace": (_sz, [_i, _i64, _i64, _i64, _i64, _i64, _i64]),
     "onionop_flash_attn_bwd": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
                                     _vp, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp, _vp, _sz]),
+    "onionop_flash_attn_bwd_noalloc": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
+                                            _vp, _vp, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp]),
     "onionop_flash_attn_bwd_preprocess": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz]),
     "onionop_flash_attn_bwd_dkdv": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                          _vp, _i, _f, _i, _vp, _vp, _vp, _sz]),
