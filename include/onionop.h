@@ -47,7 +47,7 @@ enum onionop_status {
     ONIONOP_OK = 0,
     ONIONOP_E_SHAPE = -1,        /* shape / size mismatch (reference `error(...)`, `@assert`) */
     ONIONOP_E_DTYPE = -2,        /* unknown or unsupported element type                       */
-    ONIONOP_E_UNSUPPORTED = -3,  /* valid request this build has no kernel for (e.g. E=256)   */
+    ONIONOP_E_UNSUPPORTED = -3,  /* valid request this build has no kernel for (e.g. E=512)   */
     ONIONOP_E_HIP = -4,          /* a HIP runtime call failed                                  */
     ONIONOP_E_NULL = -5,         /* a required pointer is NULL                                 */
     ONIONOP_E_WORKSPACE = -6     /* workspace missing or smaller than the *_workspace() size   */
@@ -80,7 +80,7 @@ int onionop_device_lds_bytes(int device, size_t* bytes_out /* host pointer */);
  *   ms, ls (QL, QH, B)         float32 outputs: running row max and row denominator of
  *                              the online softmax, carried to the backward
  * scale multiplies Q.K before the bias; the reference passes T(1/sqrt(E))
- * (src/attention.jl:166).  E must be a power of two in {16, 32, 64, 128};
+ * (src/attention.jl:166).  E must be a power of two in {16, 32, 64, 128, 256};
  * QH % KH == 0 (q head j uses kv head j / (QH/KH), src/attention.jl:36).
  * Limits of this build (ONIONOP_E_UNSUPPORTED beyond them): L * E * sizeof(T) < 2^31
  * bytes per (head, batch) slice of q/k/v, and with a bias 64 * QL * QH * sizeof(T) < 2^32

@@ -52,9 +52,9 @@ int check_attn(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t
     if (KH == 0 || QH % KH != 0)
         return fail(ONIONOP_E_SHAPE, "Number of query heads `%lld` must be divisible by number of KV heads `%lld`.",
                     (long long)QH, (long long)KH);
-    if (E < 16 || E > 128)
-        return fail(ONIONOP_E_UNSUPPORTED, "flash_attention: embedding dim %lld not supported (16, 32, 64 or 128)",
-                    (long long)E);
+    if (E < 16 || E > 256)
+        return fail(ONIONOP_E_UNSUPPORTED,
+                    "flash_attention: embedding dim %lld not supported (16, 32, 64, 128 or 256)", (long long)E);
     if (QL > (1LL << 30) || KL > (1LL << 30) || QH > 65535 || B > 65535)
         return fail(ONIONOP_E_UNSUPPORTED, "flash_attention: dimensions too large");
     // The kernels address one (head, batch) slice of q/k/v with 32-bit byte offsets.

@@ -129,6 +129,21 @@ def test_fp32_qk_fp16_mode_no_bias(dev, causal):
     run_case(dev, "f32", 64, 300, 300, 2, 2, 2, causal, False, False, seed=5, qk16=True)
 
 
+# E = 256 (the largest head dim the reference's group-size search admits on a 64 KiB-LDS
+# device, src/attention.jl:213-225): one wave per SIMD; float32 and the bias paths use
+# scratch for part of their registers.
+@pytest.mark.parametrize("case", [
+    ("bf16", 256, 130, 130, 2, 2, 1, True, False, False),
+    ("bf16", 256, 257, 200, 4, 2, 2, False, False, True),
+    ("f16", 256, 100, 100, 2, 1, 1, True, True, False),
+    ("f32", 256, 70, 70, 2, 2, 1, False, True, True),
+    ("f32", 256, 96, 96, 2, 2, 1, True, False, False),
+], ids=lambda c: "-".join(map(str, c)))
+def test_head_dim_256(dev, case):
+    dt, E, QL, KL, QH, KH, B, causal, pair, kpad = case
+    run_case(dev, dt, E, QL, KL, QH, KH, B, causal, pair, kpad, seed=zlib.crc32(repr(case).encode()) % 1000)
+
+
 def test_fully_masked_rows(dev):
     """A batch whose keys are all padded: o = 0, ms = -Inf, ls = 0 and finite gradients
     (the reference gives NaN there)."""
@@ -186,8 +201,8 @@ def test_errors_match_reference_messages(dev):
         nnop.flash_attention(x, x, x, causal=False)
     with pytest.raises(ValueError, match="must be the same as of K"):
         nnop.flash_attention(torch.zeros((1, 2, 8, 32), device=dev), k, k, causal=False)
-    with pytest.raises(nnop.NNopError):
-        x = torch.zeros((1, 2, 8, 256), device=dev)
+    with pytest.raises(nnop.NNopError, match="embedding dim 512 not supported"):
+        x = torch.zeros((1, 2, 8, 512), device=dev)
         nnop.flash_attention(x, x, x, causal=False)
 
 
