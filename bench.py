@@ -460,6 +460,64 @@ def workloads(torch, nnop, dev):
     return out
 
 
+def counter_summary(paths, last=20):
+    """Per-kernel averages of rocprofv3 --pmc counter CSVs (the last `last` dispatches of each
+    kernel, i.e. the timed steps), with the derived utilisations:
+      mfma_busy  = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 * 1024)
+                   (MFMA-busy cycles summed over the 1024 SIMDs, over the kernel's active
+                   cycles; rocprofv3 sums GRBM_GUI_ACTIVE over the 8 XCDs)
+      valu_busy  = 4 * SQ_ACTIVE_INST_VALU / (GRBM_GUI_ACTIVE / 8 * 1024)   (quad-cycles)
+      coexec     = SQ_VALU_MFMA_COEXEC_CYCLES / (GRBM_GUI_ACTIVE / 8 * 1024)
+      lds_active = SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE / 8 * 256)          (per CU)
+      bank_conflict_share = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE
+      valu_per_mfma = SQ_INSTS_VALU / SQ_INSTS_MFMA"""
+    import csv
+    import re
+
+    def short(mangled):  # last name of an Itanium nested name: _ZN7onionop20attn_fwd_pipe_kernelI...
+        if not mangled.startswith("_ZN"):
+            return None  # torch's own kernels
+        pos, last = 3, None
+        while pos < len(mangled) and mangled[pos].isdigit():
+            end = pos
+            while mangled[end].isdigit():
+                end += 1
+            n = int(mangled[pos:end])
+            last = mangled[end:end + n]
+            pos = end + n
+        args = mangled[pos:].split("EEEv")[0] if pos < len(mangled) else ""
+        return f"{last}<{args}>" if args else last  # template arguments keep instantiations apart
+
+    acc = {}
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            name = short(r["Kernel_Name"])
+            if name is None:  # torch's own kernels
+                continue
+            acc.setdefault(name, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    out = {}
+    for name, cs in acc.items():
+        avg = {c: sum(v[-last:]) / len(v[-last:]) for c, v in cs.items()}
+        d = {c: round(x, 1) for c, x in sorted(avg.items())}
+        gui = avg.get("GRBM_GUI_ACTIVE")
+        if gui:
+            simd = gui / 8 * 1024
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in avg:
+                d["mfma_busy"] = round(avg["SQ_VALU_MFMA_BUSY_CYCLES"] / simd, 4)
+            if "SQ_ACTIVE_INST_VALU" in avg:
+                d["valu_busy"] = round(4 * avg["SQ_ACTIVE_INST_VALU"] / simd, 4)
+            if "SQ_VALU_MFMA_COEXEC_CYCLES" in avg:
+                d["coexec"] = round(avg["SQ_VALU_MFMA_COEXEC_CYCLES"] / simd, 4)
+            if "SQ_LDS_IDX_ACTIVE" in avg:
+                d["lds_active"] = round(avg["SQ_LDS_IDX_ACTIVE"] / (gui / 8 * 256), 4)
+        if avg.get("SQ_LDS_IDX_ACTIVE") and "SQ_LDS_BANK_CONFLICT" in avg:
+            d["bank_conflict_share"] = round(avg["SQ_LDS_BANK_CONFLICT"] / avg["SQ_LDS_IDX_ACTIVE"], 4)
+        if avg.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in avg:
+            d["valu_per_mfma"] = round(avg["SQ_INSTS_VALU"] / avg["SQ_INSTS_MFMA"], 2)
+        out[name] = d
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -476,7 +534,12 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run 3 plain device copies of MIB MiB (a known-size kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--counter-summary", nargs="+", metavar="CSV",
+                    help="summarise rocprofv3 --pmc counter CSVs per kernel (no GPU needed) and exit")
     args = ap.parse_args()
+    if args.counter_summary:
+        print(json.dumps(counter_summary(args.counter_summary), indent=1))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
         sys.exit(2)
