@@ -116,6 +116,16 @@ class AttnStep:
                                                p(self.kpad), self.causal, self.scale, self.qk16, p(self.dq),
                                                p(self.dk), p(self.dv), p(self.dpair), p(self.ws), self.wsb))
 
+    def bwd_rope(self, cos, sin):
+        """The combined backward with ∇llama_rope fused into the dQ / dK epilogues (q, k are
+        the rotated tensors; dq, dk come out w.r.t. the tensors before the rotation)."""
+        p = self.ptr
+        self.chk(self.L.onionop_flash_attn_bwd_rope(self.stream, self.dt, *self.dims, p(self.do), p(self.o),
+                                                    p(self.ms), p(self.ls), p(self.q), p(self.k), p(self.v),
+                                                    p(self.pair), p(self.kpad), p(cos), p(sin), self.causal,
+                                                    self.scale, self.qk16, p(self.dq), p(self.dk), p(self.dv),
+                                                    p(self.dpair), p(self.ws), self.wsb))
+
     def step(self):
         self.fwd()
         self.bwd()
@@ -154,6 +164,18 @@ class VarlenStep:
                                                       p(self.do), p(self.o), p(self.ms), p(self.ls), p(self.q),
                                                       p(self.k), p(self.v), self.causal, self.scale, 0, p(self.dq),
                                                       p(self.dk), p(self.dv), p(self.ws), self.wsb))
+
+    def step_rope(self, cos, sin):
+        """step() with ∇llama_rope fused into the backward (cos / sin one row per packed position)."""
+        p, m = self.ptr, self.max_len
+        self.chk(self.L.onionop_flash_attn_varlen_fwd(self.stream, self.dt, *self.dims, p(self.cu), p(self.cu), m, m,
+                                                      p(self.q), p(self.k), p(self.v), self.causal, self.scale,
+                                                      p(self.o), p(self.ms), p(self.ls)))
+        self.chk(self.L.onionop_flash_attn_varlen_bwd_rope(self.stream, self.dt, *self.dims, p(self.cu), p(self.cu),
+                                                           m, m, p(self.do), p(self.o), p(self.ms), p(self.ls),
+                                                           p(self.q), p(self.k), p(self.v), p(cos), p(sin),
+                                                           self.causal, self.scale, 0, p(self.dq), p(self.dk),
+                                                           p(self.dv), p(self.ws), self.wsb))
 
 
 def time_region(torch, fn, iters):
@@ -361,7 +383,8 @@ def workloads(torch, nnop, dev):
               can sit in the 256 MB MALL);
       gqa     llama_rope + causal GQA flash attention bf16 (128,8192,32:8,4) with per-sequence
               lengths U[1024,8192] (seed 4) as a key-padding mask + llama_rope backward, and the
-              same sequences packed (variable-length entry points, RoPE positions per sequence).
+              same sequences packed (variable-length entry points, RoPE positions per sequence);
+              each also with ∇llama_rope fused into the attention backward (…_fused_rope_bwd).
     Rates of the GQA lines count valid work only (7 QH E sum(len^2))."""
     import numpy as np
     from nnop import _lib
@@ -431,6 +454,18 @@ def workloads(torch, nnop, dev):
         "lens": lens.tolist(), "us": round(t), "TFLOP/s_valid_work": round(fl / t / 1e6, 1),
         "frac_of_bf16_mfma": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 4)}
     log(f"  gqa keymask: {t:.0f} us  {fl / t / 1e6:.0f} TFLOP/s (valid work)")
+
+    def gqa_step_fused():  # the same step, ∇llama_rope fused into the attention backward
+        _lib.check(L.onionop_llama_rope(stream, 2, E, QL, QH, KH, B, ptr(q), ptr(k), ptr(cos), ptr(sin), 1.0,
+                                        ptr(qr), ptr(kr)))
+        st.fwd()
+        st.bwd_rope(cos, sin)
+
+    t = timed(gqa_step_fused, 6)
+    out["gqa_rope_bf16_128x8192x32:8x4_keymask_fused_rope_bwd"] = {
+        "us": round(t), "TFLOP/s_valid_work": round(fl / t / 1e6, 1),
+        "frac_of_bf16_mfma": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 4)}
+    log(f"  gqa keymask, fused rope bwd: {t:.0f} us  {fl / t / 1e6:.0f} TFLOP/s (valid work)")
     del st, qr, kr, dqr, dkr
 
     # the same sequences packed: (QH, sum(len), E); RoPE positions restart per sequence
@@ -457,6 +492,17 @@ def workloads(torch, nnop, dev):
         "lens": lens.tolist(), "us": round(t), "TFLOP/s_valid_work": round(fl / t / 1e6, 1),
         "frac_of_bf16_mfma": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 4)}
     log(f"  gqa packed: {t:.0f} us  {fl / t / 1e6:.0f} TFLOP/s (valid work)")
+
+    def packed_step_fused():
+        _lib.check(L.onionop_llama_rope(stream, 2, E, Tq, QH, KH, 1, ptr(qp), ptr(kpk), ptr(cosp), ptr(sinp), 1.0,
+                                        ptr(qrp), ptr(krp)))
+        vst.step_rope(cosp, sinp)
+
+    t = timed(packed_step_fused, 6)
+    out["gqa_rope_bf16_128x8192x32:8x4_packed_fused_rope_bwd"] = {
+        "us": round(t), "TFLOP/s_valid_work": round(fl / t / 1e6, 1),
+        "frac_of_bf16_mfma": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 4)}
+    log(f"  gqa packed, fused rope bwd: {t:.0f} us  {fl / t / 1e6:.0f} TFLOP/s (valid work)")
     return out
 
 

@@ -207,6 +207,43 @@ int onionop_flash_attn_varlen_bwd(void* stream, int dtype,
                                   const void* q, const void* k, const void* v, int causal, float scale, int qk_fp16,
                                   void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes);
 
+/*
+ * ∇flash_attention followed by ∇llama_rope in one backward: the pullback of
+ * flash_attention(llama_rope(q, k; cos, sin)..., v) for the rrules of both
+ * (src/attention_crc.jl:16-31, src/rope/llama_rope.jl:94-98).  Arguments as
+ * onionop_flash_attn_bwd, with q and k the rotated tensors the forward used (the output of
+ * onionop_llama_rope), and cos / sin (B, L, E) float32 the tables of that rotation
+ * (QL == KL == L); dq and dk come out w.r.t. the tensors before the rotation, as the
+ * reference's ∇llama_rope (sin_sign = -1) would give them.  The rotation is applied to the
+ * float32 dQ / dK accumulators before they are stored, so no separate pass over dq and dk
+ * runs.  No counterpart launcher in the reference: it composes the two rrules.
+ */
+int onionop_flash_attn_bwd_rope(void* stream, int dtype,
+                                int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B,
+                                const void* dO, const void* o, const float* ms, const float* ls,
+                                const void* q, const void* k, const void* v,
+                                const void* pair, const uint8_t* kpad,
+                                const float* cos, const float* sin,
+                                int causal, float scale, int qk_fp16,
+                                void* dq, void* dk, void* dv, void* dpair,
+                                void* workspace, size_t workspace_bytes);
+
+/*
+ * The same for packed sequences: onionop_flash_attn_varlen_bwd with the fused ∇llama_rope.
+ * q and k must be packed alike (cu_seqlens_q == cu_seqlens_k, Tq == Tk); cos / sin are
+ * (Tq, E) float32, one row per packed position (positions restart per sequence).
+ */
+int onionop_flash_attn_varlen_bwd_rope(void* stream, int dtype,
+                                       int64_t E, int64_t Tq, int64_t Tk, int64_t QH, int64_t KH, int64_t B,
+                                       const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                       int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                       const void* dO, const void* o, const float* ms, const float* ls,
+                                       const void* q, const void* k, const void* v,
+                                       const float* cos, const float* sin,
+                                       int causal, float scale, int qk_fp16,
+                                       void* dq, void* dk, void* dv,
+                                       void* workspace, size_t workspace_bytes);
+
 /* -------------------------------------------------------------------- softmax */
 
 /*
@@ -308,6 +345,16 @@ int onionop_llama_rope(void* stream, int dtype, int64_t E, int64_t L,
                        int64_t QH, int64_t KH, int64_t B,
                        const void* q, const void* k, const float* cos, const float* sin,
                        float sin_sign, void* q_out, void* k_out);
+
+/*
+ * LlamaRotaryEmbedding(dim; base)(positions) on the device (src/rope/llama_rope.jl:1-22):
+ * positions (L, B) float32 (row-major (B, L)); cos, sin (dim, L, B) float32 outputs
+ * (row-major (B, L, dim)): inv_freq = 1 ./ base .^ ((0:2:dim-1) ./ dim) and
+ * freqs = inv_freq .* positions in float32 as the reference computes them, then
+ * cos / sin of vcat(freqs, freqs), each correctly rounded to float32.  dim must be even.
+ */
+int onionop_llama_rotary_embedding(void* stream, int64_t dim, int64_t L, int64_t B, int64_t base,
+                                   const float* positions, float* cos, float* sin);
 
 #ifdef __cplusplus
 }

@@ -168,7 +168,8 @@ static int attn_bwd_common(const char* what, int stages, void* stream, int dtype
                            int64_t QH, int64_t KH, int64_t B, const void* dO, const void* o, const float* ms,
                            const float* ls, const void* q, const void* k, const void* v, const void* pair,
                            const uint8_t* kpad, int causal, float scale, int qk_fp16, void* dq, void* dk, void* dv,
-                           void* dpair, void* workspace, size_t workspace_bytes) {
+                           void* dpair, void* workspace, size_t workspace_bytes, const float* rope_cos = nullptr,
+                           const float* rope_sin = nullptr) {
     int st = check_attn(dtype, E, QL, KL, QH, KH, B);
     if (st) return st;
     if ((st = check_pair(pair, dtype, QL, QH))) return st;
@@ -201,6 +202,15 @@ static int attn_bwd_common(const char* what, int stages, void* stream, int dtype
     a.q = q; a.k = k; a.v = v; a.pair = pair; a.kpad = kpad; a.causal = causal != 0; a.scale = scale;
     a.dO = dO; a.o_in = o; a.ms_in = ms; a.ls_in = ls; a.qk_fp16 = qk_fp16 != 0;
     a.dq = dq; a.dk = dk; a.dv = dv; a.dpair = dpair;
+    if (rope_cos != nullptr || rope_sin != nullptr) {
+        if (rope_cos == nullptr || rope_sin == nullptr) return fail(ONIONOP_E_NULL, "%s: NULL cos / sin table", what);
+        if (QL != KL)
+            return fail(ONIONOP_E_SHAPE, "%s: the rotary embedding needs q and k of one length (%lld != %lld)", what,
+                        (long long)QL, (long long)KL);
+        if (B * QL * E * 4 >= (1LL << 32))
+            return fail(ONIONOP_E_UNSUPPORTED, "%s: cos / sin tables too large (B*L*E*4 must be below 2^32)", what);
+        a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.rope_rows = B * QL;
+    }
     if (need > 0) {
         uintptr_t base = (reinterpret_cast<uintptr_t>(workspace) + 255) & ~uintptr_t(255);
         const size_t rows = (size_t)QL * (size_t)QH * (size_t)B;
@@ -220,6 +230,17 @@ int onionop_flash_attn_bwd(void* stream, int dtype, int64_t E, int64_t QL, int64
     return attn_bwd_common("∇flash_attention", onionop::kBwdAll, stream, dtype, E, QL, KL, QH, KH, B, dO, o, ms, ls,
                            q, k, v, pair, kpad, causal, scale, qk_fp16, dq, dk, dv, dpair, workspace,
                            workspace_bytes);
+}
+
+int onionop_flash_attn_bwd_rope(void* stream, int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
+                                int64_t B, const void* dO, const void* o, const float* ms, const float* ls,
+                                const void* q, const void* k, const void* v, const void* pair, const uint8_t* kpad,
+                                const float* cos, const float* sin, int causal, float scale, int qk_fp16, void* dq,
+                                void* dk, void* dv, void* dpair, void* workspace, size_t workspace_bytes) {
+    const char* what = "∇flash_attention ∘ ∇llama_rope";
+    if (cos == nullptr || sin == nullptr) return fail(ONIONOP_E_NULL, "%s: NULL cos / sin table", what);
+    return attn_bwd_common(what, onionop::kBwdAll, stream, dtype, E, QL, KL, QH, KH, B, dO, o, ms, ls, q, k, v, pair,
+                           kpad, causal, scale, qk_fp16, dq, dk, dv, dpair, workspace, workspace_bytes, cos, sin);
 }
 
 int onionop_flash_attn_bwd_noalloc(void* stream, int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH,
@@ -320,13 +341,12 @@ size_t onionop_flash_attn_varlen_bwd_workspace(int dtype, int64_t E, int64_t Tq,
     return 2 * (size_t)Tq * (size_t)QH * sizeof(float) + 256;  // lse2 and delta per packed query row
 }
 
-int onionop_flash_attn_varlen_bwd(void* stream, int dtype, int64_t E, int64_t Tq, int64_t Tk, int64_t QH,
-                                  int64_t KH, int64_t B, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                  int64_t max_seqlen_q, int64_t max_seqlen_k, const void* dO, const void* o,
-                                  const float* ms, const float* ls, const void* q, const void* k, const void* v,
-                                  int causal, float scale, int qk_fp16, void* dq, void* dk, void* dv, void* workspace,
-                                  size_t workspace_bytes) {
-    const char* what = "∇flash_attention (varlen)";
+static int varlen_bwd_common(const char* what, void* stream, int dtype, int64_t E, int64_t Tq, int64_t Tk,
+                             int64_t QH, int64_t KH, int64_t B, const int32_t* cu_seqlens_q,
+                             const int32_t* cu_seqlens_k, int64_t max_seqlen_q, int64_t max_seqlen_k, const void* dO,
+                             const void* o, const float* ms, const float* ls, const void* q, const void* k,
+                             const void* v, const float* rope_cos, const float* rope_sin, int causal, float scale,
+                             int qk_fp16, void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes) {
     int st = check_varlen(what, dtype, E, Tq, Tk, QH, KH, B, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k);
     if (st) return st;
     const bool any_q = Tq * QH > 0, any_k = Tk * KH > 0;
@@ -342,6 +362,14 @@ int onionop_flash_attn_varlen_bwd(void* stream, int dtype, int64_t E, int64_t Tq
                                       q, k, v, causal, scale);
     a.dO = dO; a.o_in = o; a.ms_in = ms; a.ls_in = ls; a.qk_fp16 = qk_fp16 != 0;
     a.dq = dq; a.dk = dk; a.dv = dv; a.dpair = nullptr;
+    if (rope_cos != nullptr || rope_sin != nullptr) {
+        if (rope_cos == nullptr || rope_sin == nullptr) return fail(ONIONOP_E_NULL, "%s: NULL cos / sin table", what);
+        if (cu_seqlens_q != cu_seqlens_k || Tq != Tk)
+            return fail(ONIONOP_E_SHAPE, "%s: the rotary embedding needs q and k packed alike (one cu_seqlens)", what);
+        if (Tq * E * 4 >= (1LL << 32))
+            return fail(ONIONOP_E_UNSUPPORTED, "%s: cos / sin tables too large (Tq*E*4 must be below 2^32)", what);
+        a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.rope_rows = Tq;
+    }
     if (need > 0) {
         uintptr_t base = (reinterpret_cast<uintptr_t>(workspace) + 255) & ~uintptr_t(255);
         a.lse2 = reinterpret_cast<float*>(base);
@@ -350,6 +378,31 @@ int onionop_flash_attn_varlen_bwd(void* stream, int dtype, int64_t E, int64_t Tq
     if (!onionop::launch_attn_bwd((hipStream_t)stream, dtype, a, onionop::kBwdAll))
         return fail(ONIONOP_E_UNSUPPORTED, "%s: no kernel for %s E=%lld", what, dt_name(dtype), (long long)E);
     return check_launch(what);
+}
+
+int onionop_flash_attn_varlen_bwd(void* stream, int dtype, int64_t E, int64_t Tq, int64_t Tk, int64_t QH,
+                                  int64_t KH, int64_t B, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int64_t max_seqlen_q, int64_t max_seqlen_k, const void* dO, const void* o,
+                                  const float* ms, const float* ls, const void* q, const void* k, const void* v,
+                                  int causal, float scale, int qk_fp16, void* dq, void* dk, void* dv, void* workspace,
+                                  size_t workspace_bytes) {
+    return varlen_bwd_common("∇flash_attention (varlen)", stream, dtype, E, Tq, Tk, QH, KH, B, cu_seqlens_q,
+                             cu_seqlens_k, max_seqlen_q, max_seqlen_k, dO, o, ms, ls, q, k, v, nullptr, nullptr, causal,
+                             scale, qk_fp16, dq, dk, dv, workspace, workspace_bytes);
+}
+
+int onionop_flash_attn_varlen_bwd_rope(void* stream, int dtype, int64_t E, int64_t Tq, int64_t Tk, int64_t QH,
+                                       int64_t KH, int64_t B, const int32_t* cu_seqlens_q,
+                                       const int32_t* cu_seqlens_k, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                       const void* dO, const void* o, const float* ms, const float* ls, const void* q,
+                                       const void* k, const void* v, const float* cos, const float* sin, int causal,
+                                       float scale, int qk_fp16, void* dq, void* dk, void* dv, void* workspace,
+                                       size_t workspace_bytes) {
+    const char* what = "∇flash_attention ∘ ∇llama_rope (varlen)";
+    if (cos == nullptr || sin == nullptr) return fail(ONIONOP_E_NULL, "%s: NULL cos / sin table", what);
+    return varlen_bwd_common(what, stream, dtype, E, Tq, Tk, QH, KH, B, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                             max_seqlen_k, dO, o, ms, ls, q, k, v, cos, sin, causal, scale, qk_fp16, dq, dk, dv,
+                             workspace, workspace_bytes);
 }
 
 // -------------------------------------------------------------------- softmax
@@ -482,6 +535,20 @@ int onionop_layer_norm_bwd(void* stream, int dtype_x, int dtype_w, int64_t emb, 
 }
 
 // ----------------------------------------------------------------------- RoPE
+
+int onionop_llama_rotary_embedding(void* stream, int64_t dim, int64_t L, int64_t B, int64_t base,
+                                   const float* positions, float* cos, float* sin) {
+    const char* what = "LlamaRotaryEmbedding";
+    if (dim < 0 || L < 0 || B < 0) return fail(ONIONOP_E_SHAPE, "%s: negative dimension", what);
+    if (dim % 2 != 0) return fail(ONIONOP_E_SHAPE, "%s: dim %lld must be even", what, (long long)dim);
+    if (base <= 0) return fail(ONIONOP_E_SHAPE, "%s: base must be positive", what);
+    if (dim * L * B > 0 && (!positions || !cos || !sin)) return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);
+    if (dim * L * B >= (1LL << 31))
+        return fail(ONIONOP_E_UNSUPPORTED, "%s: table too large (dim * L * B must be below 2^31)", what);
+    if (!onionop::launch_rope_table((hipStream_t)stream, dim, L * B, (float)base, positions, cos, sin))
+        return fail(ONIONOP_E_UNSUPPORTED, "%s: no kernel", what);
+    return check_launch(what);
+}
 
 int onionop_llama_rope(void* stream, int dtype, int64_t E, int64_t L, int64_t QH, int64_t KH, int64_t B,
                        const void* q, const void* k, const float* cos, const float* sin, float sin_sign,

@@ -296,6 +296,46 @@ __device__ __forceinline__ SeqRows seq_rows(const VarLen& vl, int b, int QH, int
     return s;
 }
 
+// The pullback of the Llama rotate-half rotation (∇llama_rope, src/rope/llama_rope.jl:24-65
+// with sin_sign = -1) applied to one row of a gradient held as C-tile registers: this
+// lane's row (a query in dQ, a key in dK) has column e = 32 eb + 8 gg + 4 h + j in register
+// acc[eb][4 gg + j].  For i < E/2, with c = cos[i], s = sin[i] of the row's position:
+//   g_i <- g_i c + g_{i+E/2} s,   g_{i+E/2} <- g_{i+E/2} c - g_i s.
+// Both columns of a pair sit in this lane (E/2 is a multiple of 8, so column i + E/2 is
+// register ((i + E/2) / 32, ((i + E/2) % 32) / 8) with the same h and j), so the rotation
+// needs no exchange.  ctab / stab are resources over the cos / sin tables (float32, E per
+// row, the first E/2 used) and row_off the byte offset of this row in them.
+template <int E, int NEB>
+__device__ __forceinline__ void rope_bwd_row(f32x16 (&acc)[NEB], rsrc_t ctab, rsrc_t stab, uint32_t row_off, int h) {
+    constexpr int HALF = E / 2;
+    static_assert(HALF % 8 == 0, "rotation pairs in whole 8-column groups");
+#pragma unroll
+    for (int eb = 0; eb < NEB; ++eb)
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+            if (32 * eb + 8 * gg >= HALF) continue;  // compile time: this group's columns are >= E/2
+            const int e0 = 32 * eb + 8 * gg;
+            const int eb2 = (e0 + HALF) / 32, gg2 = ((e0 + HALF) % 32) / 8;
+            const uint32_t off = row_off + (uint32_t)(e0 + 4 * h) * 4u;
+            const u32x4 cr = bload16(ctab, off), sr = bload16(stab, off);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float c = __uint_as_float(cr[j]), sn = __uint_as_float(sr[j]);
+                const float a = acc[eb][4 * gg + j], b2 = acc[eb2][4 * gg2 + j];
+                acc[eb][4 * gg + j] = fmaf(a, c, b2 * sn);
+                acc[eb2][4 * gg2 + j] = fmaf(b2, c, -(a * sn));
+            }
+        }
+}
+
+// Tables of the fused rotation (nullptr: none): cos / sin (rows x E) float32, a row per
+// (batch, position) -- row b L + pos for dense tensors, the packed row for packed sequences.
+struct RopeTab {
+    const float* cos;
+    const float* sin;
+    int64_t rows;
+};
+
 // Element type helpers for the float16-rounded Q/K of the reference backward.
 template <typename T, bool QK16>
 __device__ __forceinline__ T qk_round(T x) {

@@ -23,6 +23,12 @@ struct AttnArgs {
     int qk_fp16;
     void *dq, *dk, *dv, *dpair;
     float *lse2, *delta;  // workspace: log2-domain log-sum-exp and rowsum(dO o), (B, QH, QL)
+    // Fused ∇llama_rope (backward only; nullptr: none): dq and dk come out w.r.t. q and k
+    // before the rotation.  cos / sin are (rope_rows, E) float32, one row per (batch,
+    // position) -- b L + pos for dense tensors (QL == KL), the packed row for packed ones
+    // (cu_q == cu_k).
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+    int64_t rope_rows = 0;
     // Packed variable-length sequences (cu_q == nullptr: dense).  With them, B counts
     // the sequences, QL / KL are the longest lengths (they size the grids), tensors are
     // (QH, Tq, E) / (KH, Tk, E), statistics (QH, Tq), and cu_q / cu_k hold B + 1 offsets.
@@ -47,6 +53,8 @@ bool launch_ln_fwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, cons
                    const void* b, float eps, void* y, float* mu, float* rstd);
 bool launch_ln_bwd(hipStream_t s, int dt, int dtw, int64_t n, int64_t rows, const void* dy, const float* mu,
                    const float* rstd, const void* x, const void* w, void* dx, void* dw, void* db, float* ws);
+bool launch_rope_table(hipStream_t s, int64_t dim, int64_t rows, float base, const float* pos, float* cosv,
+                       float* sinv);
 bool launch_rope(hipStream_t s, int dt, int64_t E, int64_t L, int64_t QH, int64_t KH, int64_t B, const void* q,
                  const void* k, const float* cosv, const float* sinv, float sign, void* qo, void* ko);
 

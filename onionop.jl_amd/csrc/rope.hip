@@ -121,6 +121,38 @@ static void rope_launch(hipStream_t s, const void* q, const void* k, const float
                                                  L, QH, KH, rows_per_wg, tpr);
 }
 
+// cos / sin tables of LlamaRotaryEmbedding(dim; base) at float32 positions (B, L)
+// (src/rope/llama_rope.jl:1-22): inv_freq[i] = 1 / base^(2i / dim) and freqs = inv_freq pos
+// in float32 as the reference computes them; cos / sin of freqs, written at i and again at
+// i + dim/2 (vcat(freqs, freqs)).  The power and the cos / sin are evaluated in float64 and
+// rounded once, so each table value is the correctly rounded float32 of its float32
+// argument.  One thread per (row, i < dim/2).
+__global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict__ pos, float* __restrict__ cosv,
+                                                         float* __restrict__ sinv, int64_t dim, int64_t rows,
+                                                         float base) {
+    const int64_t half = dim / 2;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= rows * half) return;
+    const int64_t r = t / half, i = t - r * half;
+    const float id = (float)(2 * i) / (float)dim;
+    const float p = (float)pow((double)base, (double)id);
+    const float inv_freq = 1.0f / p;
+    const float f = inv_freq * pos[r];
+    const float c = (float)cos((double)f), sn = (float)sin((double)f);
+    cosv[r * dim + i] = c;
+    cosv[r * dim + i + half] = c;
+    sinv[r * dim + i] = sn;
+    sinv[r * dim + i + half] = sn;
+}
+
+bool launch_rope_table(hipStream_t s, int64_t dim, int64_t rows, float base, const float* pos, float* cosv,
+                       float* sinv) {
+    const int64_t n = rows * (dim / 2);
+    if (n == 0) return true;
+    rope_table_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(pos, cosv, sinv, dim, rows, base);
+    return true;
+}
+
 bool launch_rope(hipStream_t s, int dt, int64_t E, int64_t L, int64_t QH, int64_t KH, int64_t B, const void* q,
                  const void* k, const float* cosv, const float* sinv, float sign, void* qo, void* ko) {
     if (L == 0 || B == 0 || (QH == 0 && KH == 0)) return true;

@@ -211,6 +211,85 @@ function CRC.rrule(::typeof(flash_attention_varlen), q, k, v, cu_q, cu_k, max_q,
     return o, _pullback
 end
 
+# flash_attention(llama_rope(q, k; cos, sin)..., v) with ∇llama_rope fused into the attention
+# backward: the library rotates the float32 dQ / dK accumulators before it stores them, so the
+# pullback of the composition (src/attention_crc.jl:16-31 then src/rope/llama_rope.jl:94-98)
+# runs no separate ∇llama_rope pass.  q, k are the tensors before the rotation; cos, sin
+# (E, L, B) Float32 as LlamaRotaryEmbedding returns them.
+function ∇flash_attention_rope(
+    Δ::ROCArray{T,4}, o::ROCArray{T,4}, ms::ROCArray{Float32,3}, ls::ROCArray{Float32,3},
+    qr::ROCArray{T,4}, kr::ROCArray{T,4}, v::ROCArray{T,4}, cos::ROCArray{Float32,3}, sin::ROCArray{Float32,3},
+    pair::Union{Nothing,ROCArray{T,4}} = nothing;
+    causal::Bool, kpad_mask::Union{Nothing,ROCMatrix{Bool}} = nothing,
+) where {T <: HipFloat}
+    Δ, o, qr, kr, v = _aligned(Δ), _aligned(o), _aligned(qr), _aligned(kr), _aligned(v)
+    QE, QL, QH, B = size(qr)
+    KE, KL, KH, _ = size(kr)
+    ws_bytes = ccall((:onionop_flash_attn_bwd_workspace, libonionop), Csize_t,
+                     (Cint, Int64, Int64, Int64, Int64, Int64, Int64), _dt(T), QE, QL, KL, QH, KH, B)
+    ws = ROCArray{UInt8}(undef, max(ws_bytes, 1))
+    dq, dk, dv = similar(qr), similar(kr), similar(v)
+    dpair = pair === nothing ? nothing : similar(pair)
+    _check(ccall((:onionop_flash_attn_bwd_rope, libonionop), Cint,
+        (Ptr{Cvoid}, Cint, Int64, Int64, Int64, Int64, Int64, Int64,
+         Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cfloat}, Ptr{Cfloat}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+         Ptr{Cvoid}, Ptr{UInt8}, Ptr{Cfloat}, Ptr{Cfloat}, Cint, Cfloat, Cint,
+         Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Csize_t),
+        _stream(), _dt(T), QE, QL, KL, QH, KH, B,
+        Δ, o, ms, ls, qr, kr, v, _ptr(pair), _ptr(kpad_mask), cos, sin, Cint(causal), _attn_scale(T, QE),
+        Cint(!_exact_qk()), dq, dk, dv, _ptr(dpair), ws, ws_bytes))
+    return dq, dk, dv, dpair
+end
+
+"""
+    flash_attention_rope(q, k, v, cos, sin, pair = nothing; causal, kpad_mask = nothing)
+
+`flash_attention(llama_rope(q, k; cos, sin)..., v, pair; causal, kpad_mask)` whose pullback
+fuses ∇llama_rope into the attention backward.  Differentiable in q, k, v and pair.
+"""
+function flash_attention_rope(q, k, v, cos, sin, pair = nothing; causal::Bool, kpad_mask = nothing)
+    qr, kr = NNop.llama_rope(q, k; cos, sin)
+    return first(NNop._flash_attention(qr, kr, v, pair; causal, kpad_mask))
+end
+
+function CRC.rrule(::typeof(flash_attention_rope), q, k, v, cos, sin, pair = nothing;
+                   causal::Bool, kpad_mask = nothing)
+    qr, kr = NNop.llama_rope(q, k; cos, sin)
+    o, ms, ls = NNop._flash_attention(qr, kr, v, pair; causal, kpad_mask)
+    function _pullback(Δ)
+        dq, dk, dv, dpair = ∇flash_attention_rope(_dense(CRC.unthunk(Δ), o), o, ms, ls, qr, kr, v, cos, sin, pair;
+                                                  causal, kpad_mask)
+        nt = CRC.NoTangent()
+        # one tangent per argument passed: pair only when it was given
+        return pair === nothing ? (nt, dq, dk, dv, nt, nt) : (nt, dq, dk, dv, nt, nt, dpair)
+    end
+    return o, _pullback
+end
+
+# Packed sequences with the fused ∇llama_rope: q and k packed alike (cu_q == cu_k);
+# cos, sin (E, Tq) Float32, one column per packed position.
+function flash_attention_varlen_bwd_rope(Δ::ROCArray{T,3}, o::ROCArray{T,3}, ms::ROCMatrix{Float32},
+                                         ls::ROCMatrix{Float32}, qr::ROCArray{T,3}, kr::ROCArray{T,3},
+                                         v::ROCArray{T,3}, cos::ROCMatrix{Float32}, sin::ROCMatrix{Float32},
+                                         cu::ROCVector{Int32}, max_len::Integer; causal::Bool) where {T <: HipFloat}
+    Δ, o, qr, kr, v = _aligned(Δ), _aligned(o), _aligned(qr), _aligned(kr), _aligned(v)
+    E, Tq, QH = size(qr)
+    _, Tk, KH = size(kr)
+    B = length(cu) - 1
+    ws_bytes = ccall((:onionop_flash_attn_varlen_bwd_workspace, libonionop), Csize_t,
+                     (Cint, Int64, Int64, Int64), _dt(T), E, Tq, QH)
+    ws = ROCArray{UInt8}(undef, max(ws_bytes, 1))
+    dq, dk, dv = AMDGPU.zeros(T, size(qr)), AMDGPU.zeros(T, size(kr)), AMDGPU.zeros(T, size(v))
+    _check(ccall((:onionop_flash_attn_varlen_bwd_rope, libonionop), Cint,
+        (Ptr{Cvoid}, Cint, Int64, Int64, Int64, Int64, Int64, Int64, Ptr{Int32}, Ptr{Int32}, Int64, Int64,
+         Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cfloat}, Ptr{Cfloat}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+         Ptr{Cfloat}, Ptr{Cfloat}, Cint, Cfloat, Cint,
+         Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Csize_t),
+        _stream(), _dt(T), E, Tq, Tk, QH, KH, B, cu, cu, max_len, max_len, Δ, o, ms, ls, qr, kr, v,
+        cos, sin, Cint(causal), _attn_scale(T, E), Cint(!_exact_qk()), dq, dk, dv, ws, ws_bytes))
+    return dq, dk, dv
+end
+
 # ------------------------------------------------------------------------ softmax
 
 function NNop.online_softmax(x::ROCMatrix{T}) where {T <: HipFloat}
@@ -312,6 +391,18 @@ function NNop.∇layer_norm(Δ, μ::ROCVector{Float32}, rstd::ROCVector{Float32}
 end
 
 # ------------------------------------------------------------------------ RoPE
+
+# LlamaRotaryEmbedding on device positions (src/rope/llama_rope.jl:14-22): the tables come
+# from the library's kernel, in the reference's Float32 arithmetic, each value rounded once.
+function (emb::NNop.LlamaRotaryEmbedding)(position_ids::ROCMatrix{Float32})
+    L, B = size(position_ids)
+    c = ROCArray{Float32}(undef, emb.dim, L, B)
+    s = ROCArray{Float32}(undef, emb.dim, L, B)
+    _check(ccall((:onionop_llama_rotary_embedding, libonionop), Cint,
+        (Ptr{Cvoid}, Int64, Int64, Int64, Int64, Ptr{Cfloat}, Ptr{Cfloat}, Ptr{Cfloat}),
+        _stream(), emb.dim, L, B, emb.base, position_ids, c, s))
+    return c, s
+end
 
 # q (E, L, QH, B), k (E, L, KH, B); cos, sin (E, L, B) Float32 (rows 1..E/2 are read).
 function NNop._llama_rope(q::ROCArray{T,4}, k::ROCArray{T,4}, cos::ROCArray{Float32,3}, sin::ROCArray{Float32,3};

@@ -16,22 +16,27 @@ Reference names -> here:
   NNop.rms_norm / _rms_norm / ∇rms_norm -> rms_norm / _rms_norm / grad_rms_norm
   NNop.layer_norm / _layer_norm / ∇layer_norm -> layer_norm / _layer_norm / grad_layer_norm
   NNop.llama_rope / _llama_rope / ∇llama_rope / LlamaRotaryEmbedding -> same names
+  (LlamaRotaryEmbedding on device positions: rotary_tables, the library's table kernel)
+  flash_attention(llama_rope(q, k)..., v) with the RoPE backward fused into the attention
+  backward -> flash_attention_rope / grad_flash_attention_rope (+ _varlen_rope)
 """
 from ._lib import LIB_PATH, NNopError, lib
 from .attention import (_flash_attention, _flash_attention_varlen, attention_scale, flash_attention,
-                        flash_attention_varlen, grad_flash_attention, grad_flash_attention_varlen)
+                        flash_attention_rope, flash_attention_varlen, grad_flash_attention, grad_flash_attention_rope,
+                        grad_flash_attention_varlen, grad_flash_attention_varlen_rope)
 from .norms import _layer_norm, _rms_norm, grad_layer_norm, grad_rms_norm, layer_norm, rms_norm
-from .rope import LlamaRotaryEmbedding, _llama_rope, grad_llama_rope, llama_rope
+from .rope import LlamaRotaryEmbedding, _llama_rope, grad_llama_rope, llama_rope, rotary_tables
 from .softmax import _online_softmax, grad_online_softmax, grad_online_softmax_pullback, online_softmax
 
 __all__ = [
     "LIB_PATH", "NNopError", "lib",
     "flash_attention", "_flash_attention", "grad_flash_attention", "attention_scale",
     "flash_attention_varlen", "_flash_attention_varlen", "grad_flash_attention_varlen",
+    "flash_attention_rope", "grad_flash_attention_rope", "grad_flash_attention_varlen_rope",
     "online_softmax", "_online_softmax", "grad_online_softmax", "grad_online_softmax_pullback",
     "rms_norm", "_rms_norm", "grad_rms_norm",
     "layer_norm", "_layer_norm", "grad_layer_norm",
-    "llama_rope", "_llama_rope", "grad_llama_rope", "LlamaRotaryEmbedding",
+    "llama_rope", "_llama_rope", "grad_llama_rope", "LlamaRotaryEmbedding", "rotary_tables",
     "shared_memory",
 ]
 

@@ -30,6 +30,8 @@ SIGNATURES = {
     "onionop_flash_attn_bwd_workspace": (_sz, [_i, _i64, _i64, _i64, _i64, _i64, _i64]),
     "onionop_flash_attn_bwd": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
                                     _vp, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp, _vp, _sz]),
+    "onionop_flash_attn_bwd_rope": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
+                                         _vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp, _vp, _sz]),
     "onionop_flash_attn_bwd_noalloc": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                             _vp, _vp, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp]),
     "onionop_flash_attn_bwd_preprocess": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz]),
@@ -43,6 +45,9 @@ SIGNATURES = {
     "onionop_flash_attn_varlen_bwd": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
                                            _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp,
                                            _sz]),
+    "onionop_flash_attn_varlen_bwd_rope": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
+                                                _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp, _vp,
+                                                _vp, _vp, _sz]),
     "onionop_softmax_fwd": (_i, [_vp, _i, _i64, _i64, _vp, _vp]),
     "onionop_softmax_bwd": (_i, [_vp, _i, _i64, _i64, _vp, _vp, _vp]),
     "onionop_softmax_bwd_bwd": (_i, [_vp, _i, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
@@ -53,6 +58,7 @@ SIGNATURES = {
     "onionop_layer_norm_bwd_workspace": (_sz, [_i64, _i64]),
     "onionop_layer_norm_bwd": (_i, [_vp, _i, _i, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz]),
     "onionop_llama_rope": (_i, [_vp, _i, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _f, _vp, _vp]),
+    "onionop_llama_rotary_embedding": (_i, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
 }
 
 ABI_VERSION = 2

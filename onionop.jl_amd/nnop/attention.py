@@ -228,3 +228,88 @@ def flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: in
     """Flash attention over packed variable-length sequences (differentiable in q, k, v)."""
     return _FlashAttentionVarlenFn.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
                                          int(max_seqlen_k), bool(causal), bool(qk_fp16))
+
+
+# ---------------------------------------------------------------- fused RoPE backward
+#
+# flash_attention(llama_rope(q, k; cos, sin)..., v): the forward runs llama_rope then the
+# attention forward (the rotated q, k are kept for the backward, as the two rrules keep
+# them); the backward is one launch sequence whose dQ and dK kernels apply ∇llama_rope to
+# their float32 accumulators before storing, so no pass over dq and dk follows
+# (onionop_flash_attn_bwd_rope).  The reference composes the two rrules
+# (src/attention_crc.jl:16-31, src/rope/llama_rope.jl:94-98).
+
+def grad_flash_attention_rope(do, o, ms, ls, qr, kr, v, cos, sin, pair=None, *, causal: bool, kpad_mask=None,
+                              qk_fp16: bool = True):
+    """Gradients (dq, dk, dv, dpair) w.r.t. q, k before the rotation; qr, kr are the rotated tensors."""
+    qr, kr, v, o = (device_tensor(t, "∇flash_attention ∘ ∇llama_rope") for t in (qr, kr, v, o))
+    do = device_tensor(do, "∇flash_attention ∘ ∇llama_rope").to(qr.dtype)
+    ms, ls = (device_tensor(t, "∇flash_attention ∘ ∇llama_rope") for t in (ms, ls))
+    cos = device_tensor(cos, "∇flash_attention ∘ ∇llama_rope").to(torch.float32).contiguous()
+    sin = device_tensor(sin, "∇flash_attention ∘ ∇llama_rope").to(torch.float32).contiguous()
+    pair = None if pair is None else device_tensor(pair, "∇flash_attention ∘ ∇llama_rope")
+    kpad_mask = None if kpad_mask is None else device_tensor(kpad_mask, "∇flash_attention ∘ ∇llama_rope")
+    B, QH, QL, E, KH, KL = _check_shapes(qr, kr, v, pair, kpad_mask)
+    if cos.shape != (B, QL, E) or sin.shape != (B, QL, E):
+        raise ValueError(f"cos/sin must have Julia shape {(E, QL, B)}")
+    dt = dtype_code(qr, "∇flash_attention ∘ ∇llama_rope")
+    L = _lib.lib()
+    ws_bytes = L.onionop_flash_attn_bwd_workspace(dt, E, QL, KL, QH, KH, B)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=qr.device)
+    dq, dk, dv = torch.empty_like(qr), torch.empty_like(kr), torch.empty_like(v)
+    dpair = None if pair is None else torch.empty_like(pair)
+    _lib.check(L.onionop_flash_attn_bwd_rope(
+        stream_of(qr), dt, E, QL, KL, QH, KH, B, ptr(do), ptr(o), ptr(ms), ptr(ls), ptr(qr), ptr(kr), ptr(v),
+        ptr(pair), ptr(kpad_mask), ptr(cos), ptr(sin), int(bool(causal)), attention_scale(E, qr.dtype),
+        int(bool(qk_fp16)), ptr(dq), ptr(dk), ptr(dv), ptr(dpair), ptr(ws), int(ws_bytes)))
+    return dq, dk, dv, dpair
+
+
+class _FlashAttentionRopeFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cos, sin, pair, kpad_mask, causal, qk_fp16):
+        from .rope import _llama_rope
+
+        qr, kr = _llama_rope(q, k, cos, sin, bwd=False)
+        o, ms, ls = _flash_attention(qr, kr, v, pair, causal=causal, kpad_mask=kpad_mask)
+        ctx.save_for_backward(qr, kr, v, cos, sin, pair, kpad_mask, o, ms, ls)
+        ctx.causal, ctx.qk_fp16 = causal, qk_fp16
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        qr, kr, v, cos, sin, pair, kpad_mask, o, ms, ls = ctx.saved_tensors
+        dq, dk, dv, dpair = grad_flash_attention_rope(do.contiguous(), o, ms, ls, qr, kr, v, cos, sin, pair,
+                                                      causal=ctx.causal, kpad_mask=kpad_mask, qk_fp16=ctx.qk_fp16)
+        return dq, dk, dv, None, None, dpair, None, None, None
+
+
+def flash_attention_rope(q, k, v, cos, sin, pair: Optional[torch.Tensor] = None, *, causal: bool,
+                         kpad_mask: Optional[torch.Tensor] = None, qk_fp16: bool = True):
+    """flash_attention(llama_rope(q, k; cos, sin)..., v, pair; causal, kpad_mask), differentiable in
+    q, k, v and pair, with ∇llama_rope fused into the attention backward."""
+    return _FlashAttentionRopeFn.apply(q, k, v, cos, sin, pair, kpad_mask, bool(causal), bool(qk_fp16))
+
+
+def grad_flash_attention_varlen_rope(do, o, ms, ls, qr, kr, v, cos, sin, cu_seqlens, max_seqlen: int, *,
+                                     causal: bool, qk_fp16: bool = True):
+    """Packed-sequence backward with the fused ∇llama_rope (q and k packed alike; cos / sin
+    (Tq, E) float32, one row per packed position)."""
+    what = "∇flash_attention ∘ ∇llama_rope (varlen)"
+    qr, kr, v, o = (device_tensor(t, what) for t in (qr, kr, v, o))
+    do = device_tensor(do, what).to(qr.dtype)
+    cos = device_tensor(cos, what).to(torch.float32).contiguous()
+    sin = device_tensor(sin, what).to(torch.float32).contiguous()
+    QH, Tq, E, KH, Tk, B = _check_varlen(qr, kr, v, cu_seqlens, cu_seqlens)
+    if cos.shape[-2:] != (Tq, E) or sin.shape[-2:] != (Tq, E):
+        raise ValueError(f"cos/sin must have Julia shape {(E, Tq)}")
+    dt = dtype_code(qr, what)
+    L = _lib.lib()
+    ws_bytes = L.onionop_flash_attn_varlen_bwd_workspace(dt, E, Tq, QH)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=qr.device)
+    dq, dk, dv = torch.zeros_like(qr), torch.zeros_like(kr), torch.zeros_like(v)
+    _lib.check(L.onionop_flash_attn_varlen_bwd_rope(
+        stream_of(qr), dt, E, Tq, Tk, QH, KH, B, ptr(cu_seqlens), ptr(cu_seqlens), int(max_seqlen), int(max_seqlen),
+        ptr(do), ptr(o), ptr(ms), ptr(ls), ptr(qr), ptr(kr), ptr(v), ptr(cos), ptr(sin), int(bool(causal)),
+        attention_scale(E, qr.dtype), int(bool(qk_fp16)), ptr(dq), ptr(dk), ptr(dv), ptr(ws), int(ws_bytes)))
+    return dq, dk, dv

@@ -28,9 +28,25 @@ class LlamaRotaryEmbedding:
         pos = position_ids.to(torch.float32)
         if pos.dim() == 1:
             pos = pos[None]
+        if pos.is_cuda:  # on the device: the library's table kernel
+            return rotary_tables(pos, self.dim, self.base)
         freqs = pos[..., None] * self.inv_freq.to(pos.device)[None, None, :]
         freqs = torch.cat([freqs, freqs], dim=-1)
         return torch.cos(freqs).contiguous(), torch.sin(freqs).contiguous()
+
+
+def rotary_tables(positions: torch.Tensor, dim: int, base: int = 10000):
+    """cos, sin (B, L, dim) float32 of LlamaRotaryEmbedding(dim; base) at device positions
+    (B, L) (src/rope/llama_rope.jl:1-22), computed by the library on the positions' device."""
+    pos = device_tensor(positions, "LlamaRotaryEmbedding").to(torch.float32).contiguous()
+    if pos.dim() != 2:
+        raise ValueError("LlamaRotaryEmbedding: positions must be (seq, batch) == torch (B, L)")
+    B, L = pos.shape
+    cos = torch.empty((B, L, dim), dtype=torch.float32, device=pos.device)
+    sin = torch.empty_like(cos)
+    _lib.check(_lib.lib().onionop_llama_rotary_embedding(stream_of(pos), int(dim), L, B, int(base), ptr(pos),
+                                                         ptr(cos), ptr(sin)))
+    return cos, sin
 
 
 def _llama_rope(q, k, cos, sin, *, bwd: bool):
