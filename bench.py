@@ -61,14 +61,14 @@ class AttnStep:
     q (B, QH, QL, E), k / v (B, KH, KL, E); pair (B, KL, QL, QH) and kpad (B, KL) bool are
     optional.  qk16 is the backward's Float16 Q/K flag (float32 only)."""
 
-    def __init__(self, torch, nnop, q, k, v, do, causal=True, pair=None, kpad=None, qk16=0):
+    def __init__(self, torch, nnop, q, k, v, do, causal=True, pair=None, kpad=None, qk16=0, dt=None):
         from nnop import _lib
         from nnop._util import dtype_code, ptr
 
         self.torch, self.L, self.ptr = torch, _lib.lib(), ptr
         self.q, self.k, self.v, self.do, self.pair, self.kpad = q, k, v, do, pair, kpad
         B, H, QL, E = q.shape
-        self.dt = dtype_code(q, "bench")
+        self.dt = dtype_code(q, "bench") if dt is None else dt  # 3: float32 through bf16x6 MFMA
         self.dims = (E, QL, k.shape[2], H, k.shape[1], B)
         self.causal, self.qk16 = int(causal), int(qk16)
         self.scale = nnop.attention_scale(E, q.dtype)
@@ -377,7 +377,8 @@ def workloads(torch, nnop, dev):
     """The other attention workloads at full size, timed through the C ABI with buffers
     allocated once (settled clocks, then HIP events on the library's stream):
       f32     flash attention f32 (64,1024,4,2) non-causal, q,k,v ~ U[0,1), dO = 1, with the
-              reference's Float16 Q/K backward (default) and with exact float32 Q/K;
+              reference's Float16 Q/K backward (default) and with exact float32 Q/K, on float32
+              MFMA and with the bf16x6 products (element type code 3);
       pair    bf16 (32,768,8,2) non-causal with a pair bias (8,768,768,2), gradients incl. the
               bias: FLOP rate and algorithmic HBM rate (inputs not rotated: the 18.9 MB bias
               can sit in the 256 MB MALL);
@@ -403,14 +404,17 @@ def workloads(torch, nnop, dev):
     q, k, v = [torch.rand((B, H, QL, E), generator=g, device=dev) for _ in range(3)]
     do = torch.ones_like(q)
     fl = 14 * B * H * QL * QL * E
-    for qk16 in (1, 0):
-        st = AttnStep(torch, nnop, q, k, v, do, causal=False, qk16=qk16)
-        t = timed(st.step, 50)
-        key = "f32_64x1024x4x2" + ("_qk16" if qk16 else "_exact")
-        out[key] = {"us": round(t, 1), "TFLOP/s": round(fl / t / 1e6, 1),
-                    "frac_of_fp32_mfma": round(fl / t / 1e6 / MI355X_FP32_MFMA_TFLOPS, 3)}
-        log(f"  {key}: {t:.1f} us  {fl / t / 1e6:.1f} TFLOP/s")
-        del st
+    for x6 in (False, True):  # float32 MFMA, then every product as six bf16 MFMA products
+        for qk16 in (1, 0):
+            st = AttnStep(torch, nnop, q, k, v, do, causal=False, qk16=qk16, dt=3 if x6 else None)
+            t = timed(st.step, 50)
+            key = "f32_64x1024x4x2" + ("_bf16x6" if x6 else "") + ("_qk16" if qk16 else "_exact")
+            out[key] = {"us": round(t, 1), "TFLOP/s": round(fl / t / 1e6, 1),
+                        "frac_of_fp32_mfma": round(fl / t / 1e6 / MI355X_FP32_MFMA_TFLOPS, 3)}
+            if x6:  # issued bf16 MFMA work: six products per float32 product
+                out[key]["frac_of_bf16_mfma_issued"] = round(6 * fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 3)
+            log(f"  {key}: {t:.1f} us  {fl / t / 1e6:.1f} TFLOP/s")
+            del st
     del q, k, v, do
 
     E, QL, H, B = 32, 768, 8, 2

@@ -41,7 +41,17 @@
 extern "C" {
 #endif
 
-enum onionop_dtype { ONIONOP_F32 = 0, ONIONOP_F16 = 1, ONIONOP_BF16 = 2 };
+/*
+ * ONIONOP_F32_BF16X6 (attention entry points only): float32 tensors, exactly as
+ * ONIONOP_F32, with every matrix product of the attention kernels computed on the bf16
+ * matrix cores.  Each float32 operand is split exactly into three bf16 parts
+ * (x = hi + mid + lo), and a product a b is accumulated in float32 from the six part
+ * products a_i b_j of order up to 2^-16 |a b|; the dropped ones are below 2^-23 |a b|,
+ * the size of one float32 rounding.  Softmax, scaling, masks and all accumulation stay
+ * float32.  No counterpart in the reference (its Float32 path uses float32 FMAs); it
+ * trades nothing measurable in accuracy for the bf16 matrix-core rate.
+ */
+enum onionop_dtype { ONIONOP_F32 = 0, ONIONOP_F16 = 1, ONIONOP_BF16 = 2, ONIONOP_F32_BF16X6 = 3 };
 
 enum onionop_status {
     ONIONOP_OK = 0,

@@ -36,16 +36,20 @@ int check_launch(const char* what) {
 }
 
 bool valid_dt(int dt) { return dt == ONIONOP_F32 || dt == ONIONOP_F16 || dt == ONIONOP_BF16; }
-size_t dt_size(int dt) { return dt == ONIONOP_F32 ? 4 : 2; }
+// attention also takes float32 computed with bf16x6 MFMA products
+bool valid_attn_dt(int dt) { return valid_dt(dt) || dt == ONIONOP_F32_BF16X6; }
+size_t dt_size(int dt) { return dt == ONIONOP_F32 || dt == ONIONOP_F32_BF16X6 ? 4 : 2; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
-const char* dt_name(int dt) { return dt == 0 ? "Float32" : dt == 1 ? "Float16" : dt == 2 ? "BFloat16" : "?"; }
+const char* dt_name(int dt) {
+    return dt == 0 ? "Float32" : dt == 1 ? "Float16" : dt == 2 ? "BFloat16" : dt == 3 ? "Float32 (bf16x6)" : "?";
+}
 
 // Shape checks of _flash_attention / ∇flash_attention (src/attention.jl:153-156,
 // src/attention_bwd.jl:224-227) plus what this build supports.
 int check_attn(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B) {
-    if (!valid_dt(dtype)) return fail(ONIONOP_E_DTYPE, "flash_attention: unsupported element type code %d", dtype);
+    if (!valid_attn_dt(dtype)) return fail(ONIONOP_E_DTYPE, "flash_attention: unsupported element type code %d", dtype);
     if (E < 0 || QL < 0 || KL < 0 || QH < 0 || KH < 0 || B < 0)
         return fail(ONIONOP_E_SHAPE, "flash_attention: negative dimension");
     if (!is_pow2(E)) return fail(ONIONOP_E_SHAPE, "Only power-of-2 embedding dims are supported.");

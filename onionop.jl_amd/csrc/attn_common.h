@@ -40,6 +40,71 @@ template <> struct Mfma<f16> {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }
 };
+#ifndef ONIONOP_X6
+#define ONIONOP_X6 0
+#endif
+#if ONIONOP_X6
+// float32 through bf16 MFMA ("bf16x6"; the translation unit attn_f32x6.hip compiles the
+// float32 kernels with this policy in namespace onionop_x6).  A float32 x is split
+// exactly into three bf16 values, x = hi + mid + lo: hi is x with its low 16 bits cleared
+// (its top 8 significand bits), mid the same of r = x - hi (exact, at most 16 significant
+// bits), and lo = r - mid (exact, at most 8 significant bits, so a bf16 value).  A product
+// a b is the six terms a_i b_j with i + j <= 2 (in units of 8 bits), each exact in the
+// float32 accumulator; the three dropped terms are below 2^-23 |a b| together, about the
+// rounding of one float32 operation.  Fragments cover KC = 16 contraction positions like
+// the 16-bit types, so a float32 dot product of 16 terms costs 6 MFMAs of 32 cycles
+// instead of 8 float32 MFMAs of 64.
+struct f32x6_frag {
+    bf16x8 hi, mid, lo;
+};
+template <> struct Mfma<float> {
+    static constexpr int KC = 16, KE = 8;
+    typedef f32x6_frag frag;
+    static __device__ __forceinline__ f32x16 mma(const frag& a, const frag& b, f32x16 c) {
+        // smallest terms first
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.lo, b.hi, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.hi, b.lo, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.mid, b.mid, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.mid, b.hi, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.hi, b.mid, c, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.hi, b.hi, c, 0, 0, 0);
+    }
+};
+// The split of 8 floats: element j of each plane is the bf16 part of x[j].
+__device__ __forceinline__ f32x6_frag split_f32x8(const float (&x)[8]) {
+    union { uint32_t u[4]; bf16x8 f; } H, Mi, L;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t a = __float_as_uint(x[2 * j]), b = __float_as_uint(x[2 * j + 1]);
+        const float ra = x[2 * j] - __uint_as_float(a & 0xFFFF0000u);
+        const float rb = x[2 * j + 1] - __uint_as_float(b & 0xFFFF0000u);
+        const uint32_t ua = __float_as_uint(ra), ub = __float_as_uint(rb);
+        const float la = ra - __uint_as_float(ua & 0xFFFF0000u);
+        const float lb = rb - __uint_as_float(ub & 0xFFFF0000u);
+        H.u[j] = (a >> 16) | (b & 0xFFFF0000u);
+        Mi.u[j] = (ua >> 16) | (ub & 0xFFFF0000u);
+        L.u[j] = (__float_as_uint(la) >> 16) | (__float_as_uint(lb) & 0xFFFF0000u);
+    }
+    f32x6_frag f;
+    f.hi = H.f;
+    f.mid = Mi.f;
+    f.lo = L.f;
+    return f;
+}
+// The 8 floats a fragment stands for (hi + mid + lo is exact in float32).
+__device__ __forceinline__ void join_f32x8(const f32x6_frag& f, float (&x)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = ((float)f.lo[j] + (float)f.mid[j]) + (float)f.hi[j];
+}
+// The fragment of the float16-rounded values (the reference's Float16 Q/K).
+__device__ __forceinline__ f32x6_frag round_f16(const f32x6_frag& f) {
+    float x[8];
+    join_f32x8(f, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = round_f16(x[j]);
+    return split_f32x8(x);
+}
+#else
 template <> struct Mfma<float> {
     static constexpr int KC = 2, KE = 1;
     typedef float frag;
@@ -47,6 +112,7 @@ template <> struct Mfma<float> {
         return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
     }
 };
+#endif
 
 __device__ __forceinline__ f32x16 zero16() {
     f32x16 z;
@@ -58,6 +124,13 @@ __device__ __forceinline__ f32x16 zero16() {
 // KE consecutive elements starting at p (LDS or global) as a fragment.
 template <typename T>
 __device__ __forceinline__ typename Mfma<T>::frag load_frag(const T* p) {
+#if ONIONOP_X6
+    if constexpr (sizeof(T) == 4) {  // 16-byte aligned: two 16-byte LDS reads, then the split
+        const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+        const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        return split_f32x8(x);
+    } else
+#endif
     if constexpr (Mfma<T>::KE == 8) {
         return *reinterpret_cast<const typename Mfma<T>::frag*>(p);
     } else {
@@ -78,6 +151,16 @@ __device__ __forceinline__ typename Mfma<T>::frag load_frag(const T* p) {
 // float32: one element X[kb + crow(c, h)][m0 + l%32].
 template <typename T>
 __device__ __forceinline__ typename Mfma<T>::frag load_frag_tr(const T* X, int S, int m0, int kb, int c, int lane) {
+#if ONIONOP_X6
+    if constexpr (sizeof(T) == 4) {  // the 8 k positions of kperm, one float each
+        const int h = lane >> 5;
+        const T* p = X + (kb + 16 * c + 4 * h) * S + m0 + (lane & 31);
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = p[((j & 3) + 8 * (j >> 2)) * S];
+        return split_f32x8(x);
+    } else
+#endif
     if constexpr (Mfma<T>::KE == 8) {
         typedef short s16x4 __attribute__((ext_vector_type(4)));
         typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -100,6 +183,14 @@ __device__ __forceinline__ typename Mfma<T>::frag load_frag_tr(const T* X, int S
 // Chunk c of a C tile (registers KE*c .. KE*c+KE-1) converted to a B fragment.
 template <typename T>
 __device__ __forceinline__ typename Mfma<T>::frag c_to_frag(const f32x16& acc, int c) {
+#if ONIONOP_X6
+    if constexpr (sizeof(T) == 4) {
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = acc[8 * c + j];
+        return split_f32x8(x);
+    } else
+#endif
     if constexpr (Mfma<T>::KE == 8) {
         typename Mfma<T>::frag f;
 #pragma unroll
@@ -107,6 +198,29 @@ __device__ __forceinline__ typename Mfma<T>::frag c_to_frag(const f32x16& acc, i
         return f;
     } else {
         return acc[c];
+    }
+}
+
+// Sum of the elements a fragment stands for.  For bf16x6 fragments, the sum of the hi
+// parts only (the float32 centring below needs some constant vector close to the mean of
+// K, not the exact mean).
+template <typename T>
+__device__ __forceinline__ float frag_sum(const typename Mfma<T>::frag& f) {
+#if ONIONOP_X6
+    if constexpr (sizeof(T) == 4) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += (float)f.hi[j];
+        return s;
+    } else
+#endif
+    if constexpr (Mfma<T>::KE == 8) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += to_f32(f[j]);
+        return s;
+    } else {
+        return f;
     }
 }
 

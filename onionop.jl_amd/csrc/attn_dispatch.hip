@@ -1,6 +1,12 @@
 // attn_dispatch.hip -- element-type dispatch of the attention launchers.
 #include "launch.h"
 
+// float32 through bf16x6 MFMA products (attn_f32x6.hip)
+namespace onionop_x6 {
+bool fwd_f32x6(hipStream_t s, const onionop::AttnArgs& a);
+bool bwd_f32x6(hipStream_t s, const onionop::AttnArgs& a, int stages);
+}  // namespace onionop_x6
+
 namespace onionop {
 
 typedef __bf16 bf16;
@@ -30,6 +36,7 @@ bool launch_attn_fwd(hipStream_t s, int dt, const AttnArgs& a) {
         case 0: return fwd_dispatch<float>(s, a);
         case 1: return fwd_dispatch<f16>(s, a);
         case 2: return fwd_dispatch<bf16>(s, a);
+        case 3: return onionop_x6::fwd_f32x6(s, a);
     }
     return false;
 }
@@ -39,7 +46,7 @@ bool launch_attn_bwd(hipStream_t s, int dt, const AttnArgs& a, int stages) {
     if (a.QL == 0) {  // no queries: dk = dv = 0
         if (!(stages & kBwdDkDv)) return true;
         const int64_t krows = a.cu_q ? a.KH * a.Tk : a.KL * a.KH * a.B;
-        const int64_t bytes = (dt == 0 ? 4 : 2) * a.E * krows;
+        const int64_t bytes = (dt == 0 || dt == 3 ? 4 : 2) * a.E * krows;
         if (bytes > 0) {
             zero_bytes_kernel<<<dim3((unsigned)((bytes + 1023) / 1024)), dim3(256), 0, s>>>(a.dk, bytes);
             zero_bytes_kernel<<<dim3((unsigned)((bytes + 1023) / 1024)), dim3(256), 0, s>>>(a.dv, bytes);
@@ -50,6 +57,7 @@ bool launch_attn_bwd(hipStream_t s, int dt, const AttnArgs& a, int stages) {
         case 0: return a.qk_fp16 ? bwd_dispatch<float, true>(s, a, stages) : bwd_dispatch<float, false>(s, a, stages);
         case 1: return bwd_dispatch<f16, false>(s, a, stages);
         case 2: return bwd_dispatch<bf16, false>(s, a, stages);
+        case 3: return onionop_x6::bwd_f32x6(s, a, stages);
     }
     return false;
 }

@@ -16,7 +16,15 @@ namespace onionop {
 // float32: one element, making the column reads of the float32 MFMA operands
 // conflict-free.
 template <typename T, int EO, bool WIDE = false> struct TileCfg { static constexpr int DS = EO + (WIDE ? 16 : 8); };
+// bf16x6 float32 (ONIONOP_X6): rows stay 16-byte aligned for the natural fragment reads.
+// WIDE: 8 floats, with which the two row halves of a transposed read (rows 4 apart) land
+// 32 banks apart; otherwise 4 (2-way conflicts on those reads), which keeps four
+// query-range groups of the float32 dK/dV kernel within the CU's LDS at E = 64.
+#if ONIONOP_X6
+template <int EO, bool WIDE> struct TileCfg<float, EO, WIDE> { static constexpr int DS = EO + (WIDE ? 8 : 4); };
+#else
 template <int EO, bool WIDE> struct TileCfg<float, EO, WIDE> { static constexpr int DS = EO + 1; };
+#endif
 
 // Waits until every outstanding vector-memory load has returned (s_waitcnt vmcnt(0)).
 // Issued once after the loads that precede a software-pipelined loop, so the compiler's
@@ -33,6 +41,15 @@ __device__ __forceinline__ rsrc_t slice_rsrc(const T* base, int nrows) {
 // resource; zero past the end of the slice.
 template <typename T>
 __device__ __forceinline__ typename Mfma<T>::frag bload_frag(rsrc_t r, uint32_t elem) {
+#if ONIONOP_X6
+    if constexpr (sizeof(T) == 4) {
+        union { u32x4 v; float f[4]; } a, b;
+        a.v = bload16(r, elem * 4u);
+        b.v = bload16(r, elem * 4u + 16u);
+        const float x[8] = {a.f[0], a.f[1], a.f[2], a.f[3], b.f[0], b.f[1], b.f[2], b.f[3]};
+        return split_f32x8(x);
+    } else
+#endif
     if constexpr (Mfma<T>::KE == 8) {
         union { u32x4 v; typename Mfma<T>::frag f; } u;
         u.v = bload16(r, elem * (uint32_t)sizeof(T));
@@ -78,7 +95,7 @@ struct TileRegs {
                 if (vi >= NR * VPR) continue;
             }
             const int row = vi / VPR, e0 = (vi % VPR) * VN;
-            if constexpr (sizeof(T) == 2) {
+            if constexpr (sizeof(T) == 2 || ONIONOP_X6) {  // 16-byte aligned rows
                 *reinterpret_cast<u32x4*>(dst + row * DS + e0) = r[i];
             } else {
                 union { u32x4 v; float f[4]; } u;

@@ -47,6 +47,13 @@ _dt(::Type{Float32}) = Cint(0)
 _dt(::Type{Float16}) = Cint(1)
 _dt(::Type{BFloat16}) = Cint(2)
 
+# Precision of Float32 attention: :float32 (Float32 MFMA products, the default) or :bf16x6
+# (every product as the six bf16 MFMA products of an exact three-way split, accumulated in
+# Float32: element type code ONIONOP_F32_BF16X6).  Set with
+# `NNopAMDGPUExt.FLOAT32_ATTENTION[] = :bf16x6`.
+const FLOAT32_ATTENTION = Ref(:float32)
+_attn_dt(::Type{T}) where {T} = T === Float32 && FLOAT32_ATTENTION[] === :bf16x6 ? Cint(3) : _dt(T)
+
 _ptr(::Nothing) = C_NULL
 _ptr(x::ROCArray) = pointer(x)
 _stream() = AMDGPU.stream().stream
@@ -99,7 +106,7 @@ function NNop._flash_attention(
         (Ptr{Cvoid}, Cint, Int64, Int64, Int64, Int64, Int64, Int64,
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{UInt8}, Cint, Cfloat,
          Ptr{Cvoid}, Ptr{Cfloat}, Ptr{Cfloat}),
-        _stream(), _dt(T), QE, QL, KL, QH, KH, B,
+        _stream(), _attn_dt(T), QE, QL, KL, QH, KH, B,
         q, k, v, _ptr(pair), _ptr(kpad_mask), Cint(causal), _attn_scale(T, QE), o, ms, ls))
     return o, ms, ls
 end
@@ -114,7 +121,7 @@ function NNop.∇flash_attention(
     QE, QL, QH, B = size(q)
     KE, KL, KH, _ = size(k)
     ws_bytes = ccall((:onionop_flash_attn_bwd_workspace, libonionop), Csize_t,
-                     (Cint, Int64, Int64, Int64, Int64, Int64, Int64), _dt(T), QE, QL, KL, QH, KH, B)
+                     (Cint, Int64, Int64, Int64, Int64, Int64, Int64), _attn_dt(T), QE, QL, KL, QH, KH, B)
     ws = ROCArray{UInt8}(undef, max(ws_bytes, 1))
     dq, dk, dv = similar(q), similar(k), similar(v)
     dpair = pair === nothing ? nothing : similar(pair)
@@ -123,7 +130,7 @@ function NNop.∇flash_attention(
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cfloat}, Ptr{Cfloat}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
          Ptr{Cvoid}, Ptr{UInt8}, Cint, Cfloat, Cint,
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Csize_t),
-        _stream(), _dt(T), QE, QL, KL, QH, KH, B,
+        _stream(), _attn_dt(T), QE, QL, KL, QH, KH, B,
         Δ, o, ms, ls, q, k, v, _ptr(pair), _ptr(kpad_mask), Cint(causal), _attn_scale(T, QE),
         Cint(!_exact_qk()),   # Float16 Q / K in the backward, as src/attention_bwd.jl:20-21
         dq, dk, dv, _ptr(dpair), ws, ws_bytes))
@@ -163,7 +170,7 @@ function flash_attention_varlen_fwd(q::ROCArray{T,3}, k::ROCArray{T,3}, v::ROCAr
     _check(ccall((:onionop_flash_attn_varlen_fwd, libonionop), Cint,
         (Ptr{Cvoid}, Cint, Int64, Int64, Int64, Int64, Int64, Int64, Ptr{Int32}, Ptr{Int32}, Int64, Int64,
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Cint, Cfloat, Ptr{Cvoid}, Ptr{Cfloat}, Ptr{Cfloat}),
-        _stream(), _dt(T), E, Tq, Tk, QH, KH, B, cu_q, cu_k, max_q, max_k, q, k, v, Cint(causal),
+        _stream(), _attn_dt(T), E, Tq, Tk, QH, KH, B, cu_q, cu_k, max_q, max_k, q, k, v, Cint(causal),
         _attn_scale(T, E), o, ms, ls))
     return o, ms, ls
 end
@@ -177,7 +184,7 @@ function flash_attention_varlen_bwd(Δ::ROCArray{T,3}, o::ROCArray{T,3}, ms::ROC
     _, Tk, KH = size(k)
     B = length(cu_q) - 1
     ws_bytes = ccall((:onionop_flash_attn_varlen_bwd_workspace, libonionop), Csize_t,
-                     (Cint, Int64, Int64, Int64), _dt(T), E, Tq, QH)
+                     (Cint, Int64, Int64, Int64), _attn_dt(T), E, Tq, QH)
     ws = ROCArray{UInt8}(undef, max(ws_bytes, 1))
     # gradient rows of queries / keys in no sequence are not written: they are zero
     dq, dk, dv = AMDGPU.zeros(T, size(q)), AMDGPU.zeros(T, size(k)), AMDGPU.zeros(T, size(v))
@@ -185,7 +192,7 @@ function flash_attention_varlen_bwd(Δ::ROCArray{T,3}, o::ROCArray{T,3}, ms::ROC
         (Ptr{Cvoid}, Cint, Int64, Int64, Int64, Int64, Int64, Int64, Ptr{Int32}, Ptr{Int32}, Int64, Int64,
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cfloat}, Ptr{Cfloat}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Cint, Cfloat, Cint,
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Csize_t),
-        _stream(), _dt(T), E, Tq, Tk, QH, KH, B, cu_q, cu_k, max_q, max_k, Δ, o, ms, ls, q, k, v,
+        _stream(), _attn_dt(T), E, Tq, Tk, QH, KH, B, cu_q, cu_k, max_q, max_k, Δ, o, ms, ls, q, k, v,
         Cint(causal), _attn_scale(T, E), Cint(!_exact_qk()), dq, dk, dv, ws, ws_bytes))
     return dq, dk, dv
 end
@@ -226,7 +233,7 @@ function ∇flash_attention_rope(
     QE, QL, QH, B = size(qr)
     KE, KL, KH, _ = size(kr)
     ws_bytes = ccall((:onionop_flash_attn_bwd_workspace, libonionop), Csize_t,
-                     (Cint, Int64, Int64, Int64, Int64, Int64, Int64), _dt(T), QE, QL, KL, QH, KH, B)
+                     (Cint, Int64, Int64, Int64, Int64, Int64, Int64), _attn_dt(T), QE, QL, KL, QH, KH, B)
     ws = ROCArray{UInt8}(undef, max(ws_bytes, 1))
     dq, dk, dv = similar(qr), similar(kr), similar(v)
     dpair = pair === nothing ? nothing : similar(pair)
@@ -235,7 +242,7 @@ function ∇flash_attention_rope(
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cfloat}, Ptr{Cfloat}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
          Ptr{Cvoid}, Ptr{UInt8}, Ptr{Cfloat}, Ptr{Cfloat}, Cint, Cfloat, Cint,
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Csize_t),
-        _stream(), _dt(T), QE, QL, KL, QH, KH, B,
+        _stream(), _attn_dt(T), QE, QL, KL, QH, KH, B,
         Δ, o, ms, ls, qr, kr, v, _ptr(pair), _ptr(kpad_mask), cos, sin, Cint(causal), _attn_scale(T, QE),
         Cint(!_exact_qk()), dq, dk, dv, _ptr(dpair), ws, ws_bytes))
     return dq, dk, dv, dpair
@@ -277,7 +284,7 @@ function flash_attention_varlen_bwd_rope(Δ::ROCArray{T,3}, o::ROCArray{T,3}, ms
     _, Tk, KH = size(kr)
     B = length(cu) - 1
     ws_bytes = ccall((:onionop_flash_attn_varlen_bwd_workspace, libonionop), Csize_t,
-                     (Cint, Int64, Int64, Int64), _dt(T), E, Tq, QH)
+                     (Cint, Int64, Int64, Int64), _attn_dt(T), E, Tq, QH)
     ws = ROCArray{UInt8}(undef, max(ws_bytes, 1))
     dq, dk, dv = AMDGPU.zeros(T, size(qr)), AMDGPU.zeros(T, size(kr)), AMDGPU.zeros(T, size(v))
     _check(ccall((:onionop_flash_attn_varlen_bwd_rope, libonionop), Cint,
@@ -285,7 +292,7 @@ function flash_attention_varlen_bwd_rope(Δ::ROCArray{T,3}, o::ROCArray{T,3}, ms
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cfloat}, Ptr{Cfloat}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
          Ptr{Cfloat}, Ptr{Cfloat}, Cint, Cfloat, Cint,
          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Csize_t),
-        _stream(), _dt(T), E, Tq, Tk, QH, KH, B, cu, cu, max_len, max_len, Δ, o, ms, ls, qr, kr, v,
+        _stream(), _attn_dt(T), E, Tq, Tk, QH, KH, B, cu, cu, max_len, max_len, Δ, o, ms, ls, qr, kr, v,
         cos, sin, Cint(causal), _attn_scale(T, E), Cint(!_exact_qk()), dq, dk, dv, ws, ws_bytes))
     return dq, dk, dv
 end

@@ -19,11 +19,15 @@ Reference names -> here:
   (LlamaRotaryEmbedding on device positions: rotary_tables, the library's table kernel)
   flash_attention(llama_rope(q, k)..., v) with the RoPE backward fused into the attention
   backward -> flash_attention_rope / grad_flash_attention_rope (+ _varlen_rope)
+  float32 attention on the bf16 matrix cores (six-term exact split; no reference
+  counterpart) -> set_float32_attention_precision("bf16x6") / float32_attention_precision
 """
 from ._lib import LIB_PATH, NNopError, lib
 from .attention import (_flash_attention, _flash_attention_varlen, attention_scale, flash_attention,
-                        flash_attention_rope, flash_attention_varlen, grad_flash_attention, grad_flash_attention_rope,
-                        grad_flash_attention_varlen, grad_flash_attention_varlen_rope)
+                        flash_attention_rope, flash_attention_varlen, float32_attention_precision,
+                        get_float32_attention_precision, grad_flash_attention, grad_flash_attention_rope,
+                        grad_flash_attention_varlen, grad_flash_attention_varlen_rope,
+                        set_float32_attention_precision)
 from .norms import _layer_norm, _rms_norm, grad_layer_norm, grad_rms_norm, layer_norm, rms_norm
 from .rope import LlamaRotaryEmbedding, _llama_rope, grad_llama_rope, llama_rope, rotary_tables
 from .softmax import _online_softmax, grad_online_softmax, grad_online_softmax_pullback, online_softmax
@@ -33,6 +37,7 @@ __all__ = [
     "flash_attention", "_flash_attention", "grad_flash_attention", "attention_scale",
     "flash_attention_varlen", "_flash_attention_varlen", "grad_flash_attention_varlen",
     "flash_attention_rope", "grad_flash_attention_rope", "grad_flash_attention_varlen_rope",
+    "set_float32_attention_precision", "get_float32_attention_precision", "float32_attention_precision",
     "online_softmax", "_online_softmax", "grad_online_softmax", "grad_online_softmax_pullback",
     "rms_norm", "_rms_norm", "grad_rms_norm",
     "layer_norm", "_layer_norm", "grad_layer_norm",

@@ -13,6 +13,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("ONIONOP_LIB") or os.path.normpath(os.path.join(_HERE, "..", "lib", "libonionop_hip.so"))
 
 F32, F16, BF16 = 0, 1, 2
+F32_BF16X6 = 3  # float32 tensors, attention products on bf16 MFMA (six-term split)
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64

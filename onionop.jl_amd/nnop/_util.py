@@ -3,7 +3,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import BF16, F16, F32
+from ._lib import BF16, F16, F32, F32_BF16X6
 
 _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -13,6 +13,18 @@ def dtype_code(t: torch.Tensor, what: str) -> int:
         return _DT[t.dtype]
     except KeyError:
         raise TypeError(f"{what}: unsupported element type {t.dtype} (float32, float16, bfloat16)") from None
+
+
+# Precision of float32 attention: "float32" (float32 MFMA) or "bf16x6" (every product as six
+# bf16 MFMA products of an exact three-way split).  Process-wide, like torch's
+# set_float32_matmul_precision.
+_F32_ATTN = ["float32"]
+
+
+def attn_dtype_code(t: torch.Tensor, what: str) -> int:
+    """Element type code of an attention call: F32_BF16X6 for float32 under "bf16x6"."""
+    dt = dtype_code(t, what)
+    return F32_BF16X6 if dt == F32 and _F32_ATTN[0] == "bf16x6" else dt
 
 
 def device_tensor(t: torch.Tensor, what: str) -> torch.Tensor:

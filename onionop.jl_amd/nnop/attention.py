@@ -15,7 +15,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._util import device_tensor, dtype_code, jdims, ptr, round_scalar, stream_of
+from ._util import _F32_ATTN, attn_dtype_code, device_tensor, jdims, ptr, round_scalar, stream_of
 
 
 def _check_shapes(q, k, v, pair, kpad_mask):
@@ -48,6 +48,39 @@ def _check_shapes(q, k, v, pair, kpad_mask):
     return B, QH, QL, QE, KH, KL
 
 
+def set_float32_attention_precision(mode: str) -> None:
+    """Precision of float32 flash attention for this process.
+
+    "float32" (default): float32 MFMA products, as the reference's float32 FMAs.
+    "bf16x6": each float32 operand is split exactly into three bf16 parts and every product
+    is accumulated in float32 from the six part products above 2^-23 relative size, on the
+    bf16 matrix cores (element type code ONIONOP_F32_BF16X6).  Softmax, masks and all sums
+    stay float32.  No counterpart in the reference."""
+    if mode not in ("float32", "bf16x6"):
+        raise ValueError(f"float32 attention precision must be 'float32' or 'bf16x6', got {mode!r}")
+    _F32_ATTN[0] = mode
+
+
+def get_float32_attention_precision() -> str:
+    return _F32_ATTN[0]
+
+
+class float32_attention_precision:
+    """Context manager: `with nnop.float32_attention_precision("bf16x6"): ...`."""
+
+    def __init__(self, mode: str):
+        self.mode, self.prev = mode, None
+
+    def __enter__(self):
+        self.prev = _F32_ATTN[0]
+        set_float32_attention_precision(self.mode)
+        return self
+
+    def __exit__(self, *exc):
+        _F32_ATTN[0] = self.prev
+        return False
+
+
 def attention_scale(E: int, dtype: torch.dtype) -> float:
     """T(1/sqrt(E)) (src/attention.jl:166)."""
     return round_scalar(1.0 / math.sqrt(E), dtype)
@@ -61,7 +94,7 @@ def _flash_attention(q, k, v, pair=None, *, causal: bool, kpad_mask=None):
     pair = None if pair is None else device_tensor(pair, "flash_attention")
     kpad_mask = None if kpad_mask is None else device_tensor(kpad_mask, "flash_attention")
     B, QH, QL, E, KH, KL = _check_shapes(q, k, v, pair, kpad_mask)
-    dt = dtype_code(q, "flash_attention")
+    dt = attn_dtype_code(q, "flash_attention")
     o = torch.empty_like(q)
     ms = torch.empty((B, QH, QL), dtype=torch.float32, device=q.device)
     ls = torch.empty((B, QH, QL), dtype=torch.float32, device=q.device)
@@ -91,7 +124,7 @@ def grad_flash_attention(do, o, ms, ls, q, k, v, pair=None, *, causal: bool, kpa
     B, QH, QL, E, KH, KL = _check_shapes(q, k, v, pair, kpad_mask)
     if do.shape != q.shape or o.shape != q.shape:
         raise ValueError("Δ and o must have the shape of q")
-    dt = dtype_code(q, "∇flash_attention")
+    dt = attn_dtype_code(q, "∇flash_attention")
     L = _lib.lib()
     ws_bytes = L.onionop_flash_attn_bwd_workspace(dt, E, QL, KL, QH, KH, B)
     ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
@@ -173,7 +206,7 @@ def _flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: i
     """Forward over packed sequences; returns (o, ms, ls)."""
     q, k, v = (device_tensor(t, "flash_attention (varlen)") for t in (q, k, v))
     QH, Tq, E, KH, Tk, B = _check_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k)
-    dt = dtype_code(q, "flash_attention (varlen)")
+    dt = attn_dtype_code(q, "flash_attention (varlen)")
     # Rows in no sequence (a packing buffer's tail, rows past max_seqlen_q) are not
     # written by the kernels: they start at zero (ls = 0 marks them as empty rows).
     o = torch.zeros_like(q)
@@ -194,7 +227,7 @@ def grad_flash_attention_varlen(do, o, ms, ls, q, k, v, cu_seqlens_q, cu_seqlens
     QH, Tq, E, KH, Tk, B = _check_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k)
     if do.shape != q.shape or o.shape != q.shape:
         raise ValueError("Δ and o must have the shape of q")
-    dt = dtype_code(q, "∇flash_attention (varlen)")
+    dt = attn_dtype_code(q, "∇flash_attention (varlen)")
     L = _lib.lib()
     ws_bytes = L.onionop_flash_attn_varlen_bwd_workspace(dt, E, Tq, QH)
     ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
@@ -252,7 +285,7 @@ def grad_flash_attention_rope(do, o, ms, ls, qr, kr, v, cos, sin, pair=None, *, 
     B, QH, QL, E, KH, KL = _check_shapes(qr, kr, v, pair, kpad_mask)
     if cos.shape != (B, QL, E) or sin.shape != (B, QL, E):
         raise ValueError(f"cos/sin must have Julia shape {(E, QL, B)}")
-    dt = dtype_code(qr, "∇flash_attention ∘ ∇llama_rope")
+    dt = attn_dtype_code(qr, "∇flash_attention ∘ ∇llama_rope")
     L = _lib.lib()
     ws_bytes = L.onionop_flash_attn_bwd_workspace(dt, E, QL, KL, QH, KH, B)
     ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=qr.device)
@@ -303,7 +336,7 @@ def grad_flash_attention_varlen_rope(do, o, ms, ls, qr, kr, v, cos, sin, cu_seql
     QH, Tq, E, KH, Tk, B = _check_varlen(qr, kr, v, cu_seqlens, cu_seqlens)
     if cos.shape[-2:] != (Tq, E) or sin.shape[-2:] != (Tq, E):
         raise ValueError(f"cos/sin must have Julia shape {(E, Tq)}")
-    dt = dtype_code(qr, what)
+    dt = attn_dtype_code(qr, what)
     L = _lib.lib()
     ws_bytes = L.onionop_flash_attn_varlen_bwd_workspace(dt, E, Tq, QH)
     ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=qr.device)

@@ -65,6 +65,12 @@ def test_c_abi_validation_errors():
     assert st == -1 and b"must be divisible by number of KV heads" in L.onionop_last_error()
     st = L.onionop_flash_attn_fwd(None, 7, 64, 8, 8, 2, 2, 1, None, None, None, None, None, 0, 1.0, None, None, None)
     assert st == -2
+    # code 3 (float32 through bf16x6 MFMA products) is an attention element type: it passes
+    # the type check and meets the NULL tensors; the row-wise ops refuse it
+    st = L.onionop_flash_attn_fwd(None, 3, 64, 8, 8, 2, 2, 1, None, None, None, None, None, 0, 1.0, None, None, None)
+    assert st == -5
+    st = L.onionop_softmax_fwd(None, 3, 64, 4, 16, 16)
+    assert st == -2
     # head dims 16..256 are built (E = 256 passes the shape checks, then meets the NULL
     # tensors); 512 and 8 are not
     st = L.onionop_flash_attn_fwd(None, 2, 256, 8, 8, 2, 2, 1, None, None, None, None, None, 0, 1.0, None, None, None)
