@@ -115,3 +115,33 @@ def test_bf16x6_autograd_and_mode(dev):
         assert rel_err(host(a), host(b)) <= 1e-5
     with pytest.raises(ValueError, match="bf16x6"):
         nnop.set_float32_attention_precision("tf32")
+
+
+@pytest.mark.parametrize("E", [64, 128])
+def test_bf16x6_fused_rope_backward(dev, E):
+    """The fused ∇llama_rope backward under bf16x6 equals the unfused composition under
+    bf16x6 (dv bit for bit), and both stay within 1e-5 of the float64 oracle."""
+    rng = np.random.default_rng(21)
+    B, QH, KH, L = 2, 4, 2, 200
+    q, _ = make(rng, (B, QH, L, E), torch.float32, dev)
+    k, _ = make(rng, (B, KH, L, E), torch.float32, dev)
+    v, vn = make(rng, (B, KH, L, E), torch.float32, dev)
+    do, don = make(rng, (B, QH, L, E), torch.float32, dev)
+    pos = torch.arange(L, dtype=torch.float32, device=dev)[None].expand(B, L).contiguous()
+    cos, sin = nnop.LlamaRotaryEmbedding(E)(pos)
+    print(f"bf16x6 fused rope E={E}", flush=True)
+    with nnop.float32_attention_precision("bf16x6"):
+        qr, kr = nnop._llama_rope(q, k, cos, sin, bwd=False)
+        o, ms, ls = nnop._flash_attention(qr, kr, v, causal=True)
+        dq, dk, dv, _ = nnop.grad_flash_attention_rope(do, o, ms, ls, qr, kr, v, cos, sin, causal=True,
+                                                       qk_fp16=False)
+        dqr2, dkr2, dv2, _ = nnop.grad_flash_attention(do, o, ms, ls, qr, kr, v, causal=True, qk_fp16=False)
+        dq2, dk2 = nnop.grad_llama_rope(dqr2, dkr2, cos=cos, sin=sin)
+    torch.cuda.synchronize()
+    assert torch.equal(dv, dv2)
+    assert rel_err(host(dq), host(dq2)) <= 1e-6 and rel_err(host(dk), host(dk2)) <= 1e-6
+    scale = nnop.attention_scale(E, torch.float32)
+    dqr_r, dkr_r, dv_r, _ = oracle.attn_bwd(don, host(qr), host(kr), vn, None, None, True, scale)
+    dq_r, dk_r = oracle.llama_rope(dqr_r, dkr_r, host(cos), host(sin), sin_sign=-1.0)
+    errs = {"dq": rel_err(host(dq), dq_r), "dk": rel_err(host(dk), dk_r), "dv": rel_err(host(dv), dv_r)}
+    assert all(e <= 1e-5 for e in errs.values()), errs
