@@ -331,10 +331,12 @@ def grad_flash_attention_varlen_rope(do, o, ms, ls, qr, kr, v, cos, sin, cu_seql
     what = "∇flash_attention ∘ ∇llama_rope (varlen)"
     qr, kr, v, o = (device_tensor(t, what) for t in (qr, kr, v, o))
     do = device_tensor(do, what).to(qr.dtype)
+    ms, ls = device_tensor(ms, what), device_tensor(ls, what)
     cos = device_tensor(cos, what).to(torch.float32).contiguous()
     sin = device_tensor(sin, what).to(torch.float32).contiguous()
     QH, Tq, E, KH, Tk, B = _check_varlen(qr, kr, v, cu_seqlens, cu_seqlens)
-    if cos.shape[-2:] != (Tq, E) or sin.shape[-2:] != (Tq, E):
+    # one table row per packed position: (Tq, E), or (1, Tq, E) as LlamaRotaryEmbedding returns it
+    if cos.numel() != Tq * E or sin.numel() != Tq * E or cos.shape[-2:] != (Tq, E) or sin.shape[-2:] != (Tq, E):
         raise ValueError(f"cos/sin must have Julia shape {(E, Tq)}")
     dt = attn_dtype_code(qr, what)
     L = _lib.lib()
