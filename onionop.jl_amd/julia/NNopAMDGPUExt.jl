@@ -221,7 +221,8 @@ end
 # flash_attention(llama_rope(q, k; cos, sin)..., v) with ∇llama_rope fused into the attention
 # backward: the library rotates the float32 dQ / dK accumulators before it stores them, so the
 # pullback of the composition (src/attention_crc.jl:16-31 then src/rope/llama_rope.jl:94-98)
-# runs no separate ∇llama_rope pass.  q, k are the tensors before the rotation; cos, sin
+# runs no separate ∇llama_rope pass.  qr, kr are the rotated tensors the forward used (the
+# output of llama_rope); dq, dk come back w.r.t. q, k before the rotation.  cos, sin
 # (E, L, B) Float32 as LlamaRotaryEmbedding returns them.
 function ∇flash_attention_rope(
     Δ::ROCArray{T,4}, o::ROCArray{T,4}, ms::ROCArray{Float32,3}, ls::ROCArray{Float32,3},
