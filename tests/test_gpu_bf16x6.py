@@ -145,3 +145,26 @@ def test_bf16x6_fused_rope_backward(dev, E):
     dq_r, dk_r = oracle.llama_rope(dqr_r, dkr_r, host(cos), host(sin), sin_sign=-1.0)
     errs = {"dq": rel_err(host(dq), dq_r), "dk": rel_err(host(dk), dk_r), "dv": rel_err(host(dv), dv_r)}
     assert all(e <= 1e-5 for e in errs.values()), errs
+
+
+def test_bf16x6_masked_edges(dev):
+    """Edge cases of the masks under bf16x6: a batch whose keys are all padded (o = 0,
+    ms = -Inf, ls = 0, finite gradients), whole padded key blocks next to partial ones,
+    and a single key (o = v exactly: P = 1 is exact in every split)."""
+    kpad = np.ones((2, 130), dtype=bool)
+    kpad[1, :] = False
+    kpad2 = np.ones((2, 200), dtype=bool)
+    kpad2[0, 64:160] = False
+    kpad2[1, 150:] = False
+    with nnop.float32_attention_precision("bf16x6"):
+        run_case(dev, "f32", 32, 70, 130, 2, 2, 2, False, True, True, seed=5, kpad=kpad)
+        for causal in (False, True):
+            run_case(dev, "f32", 64, 180, 200, 4, 2, 2, causal, False, True, seed=11, kpad=kpad2)
+        rng = np.random.default_rng(1)
+        q, _ = make(rng, (2, 2, 1, 64), torch.float32, dev)
+        k, _ = make(rng, (2, 2, 1, 64), torch.float32, dev)
+        v, _ = make(rng, (2, 2, 1, 64), torch.float32, dev)
+        o, ms, ls = nnop._flash_attention(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o, v)
+    assert torch.all(ls == 1.0)
