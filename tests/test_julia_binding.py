@@ -1,5 +1,5 @@
-"""The Julia extension (onionop.jl_amd/julia/NNopAMDGPUExt.jl) against the C ABI, without
-Julia.
+"""The two bindings of the C ABI -- the Julia extension (onionop.jl_amd/julia/NNopAMDGPUExt.jl)
+and the Python mirror's ctypes table -- against include/onionop.h, without Julia.
 
 Every `ccall` in the extension is parsed and checked against include/onionop.h and the
 built library: the symbol is declared and exported; the argument-type tuple has one entry
@@ -150,3 +150,23 @@ def test_parser_catches_a_wrong_binding():
     assert _mismatches(dropped) == ["onionop_softmax_fwd"]
     unbalanced = src.replace(call, "(Ptr{Cvoid}, Cint, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}), _stream(), _dt(T), N, M, x)")
     assert _mismatches(unbalanced) == ["onionop_softmax_fwd"]
+
+
+_CT_CLASS = {ctypes.c_void_p: "ptr", ctypes.c_char_p: "ptr", ctypes.c_int: "int", ctypes.c_int64: "int64",
+             ctypes.c_size_t: "size_t", ctypes.c_float: "float"}
+
+
+def _ct_class(t):
+    return "ptr" if isinstance(t, type) and issubclass(t, ctypes._Pointer) else _CT_CLASS[t]
+
+
+def test_python_signatures_match_the_header():
+    """The Python mirror's ctypes table (nnop._lib.SIGNATURES) against the header, by the
+    same ABI classes: every declared function is there, with its return and argument
+    classes."""
+    decls = header_decls()
+    assert set(_lib.SIGNATURES) == set(decls)
+    for name, (res, args) in _lib.SIGNATURES.items():
+        cret, cparams = decls[name]
+        assert _ct_class(res) == cret, f"{name}: return"
+        assert [_ct_class(a) for a in args] == cparams, f"{name}: arguments"
