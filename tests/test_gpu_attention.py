@@ -164,6 +164,41 @@ def test_padded_key_blocks(dev, dt, E, causal):
     run_case(dev, dt, E, 180, 200, 4, 2, 2, causal, False, True, seed=11, kpad=kpad)
 
 
+@pytest.mark.parametrize("dt,causal", [("bf16", True), ("f16", False), ("bf16", False)])
+def test_four_wave_dkdv_groups(dev, dt, causal):
+    """16-bit E = 64 without a bias on grids of at least 256 workgroups of 128 keys takes the
+    four-wave dK/dV groups: (64, 1024, 16:8, 4), GQA, with key padding that leaves one whole
+    128-key block of batch 1 padded (its workgroups write zero dK / dV without computing)
+    and the last keys of batch 2 padded.  Heads are independent, so one batch's kv group is
+    an exact sub-problem for the oracle: batches 1 and 2, kv head 5 (q heads 10, 11)."""
+    dtype = DTYPES[dt]
+    B, QH, KH, L, E = 4, 16, 8, 1024, 64
+    rng = np.random.default_rng(21)
+    q, qn = make(rng, (B, QH, L, E), dtype, dev)
+    k, kn = make(rng, (B, KH, L, E), dtype, dev)
+    v, vn = make(rng, (B, KH, L, E), dtype, dev)
+    do, don = make(rng, (B, QH, L, E), dtype, dev)
+    kpad = np.ones((B, L), dtype=bool)
+    kpad[1, 256:384] = False
+    kpad[2, -77:] = False
+    kp = torch.from_numpy(kpad).to(dev)
+    print(f"four-wave dK/dV: {dt} (64,1024,16:8,4) causal={causal} key padding", flush=True)
+    o, ms, ls = nnop._flash_attention(q, k, v, causal=causal, kpad_mask=kp)
+    dq, dk, dv, _ = nnop.grad_flash_attention(do, o, ms, ls, q, k, v, causal=causal, kpad_mask=kp)
+    torch.cuda.synchronize()
+    scale = nnop.attention_scale(E, dtype)
+    errs = {}
+    for b in (1, 2):
+        sq, sk = (slice(b, b + 1), slice(10, 12)), (slice(b, b + 1), slice(5, 6))
+        dq_r, dk_r, dv_r, _ = oracle.attn_bwd(don[sq], qn[sq], kn[sk], vn[sk], None, kpad[b:b + 1], causal, scale)
+        errs.update({f"dq{b}": rel_err(host(dq[sq]), dq_r), f"dk{b}": rel_err(host(dk[sk]), dk_r),
+                     f"dv{b}": rel_err(host(dv[sk]), dv_r)})
+    assert all(e <= TOL[dtype] for e in errs.values()), errs
+    # padded keys get exactly zero gradients, whole padded blocks included
+    assert torch.count_nonzero(dk[1, :, 256:384]) == 0 and torch.count_nonzero(dv[1, :, 256:384]) == 0
+    assert torch.count_nonzero(dk[2, :, -77:]) == 0 and torch.count_nonzero(dv[2, :, -77:]) == 0
+
+
 def test_single_key(dev):
     """L = 1: o = v exactly, whatever q."""
     rng = np.random.default_rng(1)
