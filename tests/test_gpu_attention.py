@@ -166,8 +166,9 @@ def test_padded_key_blocks(dev, dt, E, causal):
 
 @pytest.mark.parametrize("dt,causal", [("bf16", True), ("f16", False), ("bf16", False)])
 def test_four_wave_dkdv_groups(dev, dt, causal):
-    """16-bit E = 64 without a bias on grids of at least 256 workgroups of 128 keys takes the
-    four-wave dK/dV groups: (64, 1024, 16:8, 4), GQA, with key padding that leaves one whole
+    """16-bit E = 64 without a bias on grids of at least 256 workgroups of 128 keys (or
+    queries) takes the four-wave dK/dV groups, and without the causal mask the four-wave
+    forward groups: (64, 1024, 16:8, 4), GQA, with key padding that leaves one whole
     128-key block of batch 1 padded (its workgroups write zero dK / dV without computing)
     and the last keys of batch 2 padded.  Heads are independent, so one batch's kv group is
     an exact sub-problem for the oracle: batches 1 and 2, kv head 5 (q heads 10, 11)."""
@@ -190,9 +191,10 @@ def test_four_wave_dkdv_groups(dev, dt, causal):
     errs = {}
     for b in (1, 2):
         sq, sk = (slice(b, b + 1), slice(10, 12)), (slice(b, b + 1), slice(5, 6))
+        o_r, _, _ = oracle.attn_fwd(qn[sq], kn[sk], vn[sk], None, kpad[b:b + 1], causal, scale)
         dq_r, dk_r, dv_r, _ = oracle.attn_bwd(don[sq], qn[sq], kn[sk], vn[sk], None, kpad[b:b + 1], causal, scale)
-        errs.update({f"dq{b}": rel_err(host(dq[sq]), dq_r), f"dk{b}": rel_err(host(dk[sk]), dk_r),
-                     f"dv{b}": rel_err(host(dv[sk]), dv_r)})
+        errs.update({f"o{b}": rel_err(host(o[sq]), o_r), f"dq{b}": rel_err(host(dq[sq]), dq_r),
+                     f"dk{b}": rel_err(host(dk[sk]), dk_r), f"dv{b}": rel_err(host(dv[sk]), dv_r)})
     assert all(e <= TOL[dtype] for e in errs.values()), errs
     # padded keys get exactly zero gradients, whole padded blocks included
     assert torch.count_nonzero(dk[1, :, 256:384]) == 0 and torch.count_nonzero(dv[1, :, 256:384]) == 0
