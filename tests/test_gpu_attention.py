@@ -164,16 +164,19 @@ def test_padded_key_blocks(dev, dt, E, causal):
     run_case(dev, dt, E, 180, 200, 4, 2, 2, causal, False, True, seed=11, kpad=kpad)
 
 
-@pytest.mark.parametrize("dt,causal", [("bf16", True), ("f16", False), ("bf16", False)])
-def test_four_wave_dkdv_groups(dev, dt, causal):
-    """16-bit E = 64 without a bias on grids of at least 256 workgroups of 128 keys (or
-    queries) takes the four-wave dK/dV groups, and without the causal mask the four-wave
-    forward groups: (64, 1024, 16:8, 4), GQA, with key padding that leaves one whole
-    128-key block of batch 1 padded (its workgroups write zero dK / dV without computing)
-    and the last keys of batch 2 padded.  Heads are independent, so one batch's kv group is
-    an exact sub-problem for the oracle: batches 1 and 2, kv head 5 (q heads 10, 11)."""
+@pytest.mark.parametrize("dt,E,causal", [("bf16", 64, True), ("f16", 64, False), ("bf16", 64, False),
+                                         ("bf16", 128, True), ("f16", 128, False)])
+def test_four_wave_groups(dev, dt, E, causal):
+    """16-bit attention without a bias on grids of at least 256 workgroups of 128 keys (or
+    queries) takes the four-wave groups: dK/dV at E = 64, the forward and dQ at E = 128, the
+    forward at E = 64 without the causal mask.  (E, 1024, 16:KH, 4), GQA, with key padding
+    that leaves one whole 128-key block of batch 1 padded (its workgroups write zero dK / dV
+    without computing) and the last keys of batch 2 padded.  Heads are independent, so one
+    batch's kv group is an exact sub-problem for the oracle: batches 1 and 2, the kv head of
+    q head 10 with every q head of its group."""
     dtype = DTYPES[dt]
-    B, QH, KH, L, E = 4, 16, 8, 1024, 64
+    B, QH, L = 4, 16, 1024
+    KH = 8 if E == 64 else 4
     rng = np.random.default_rng(21)
     q, qn = make(rng, (B, QH, L, E), dtype, dev)
     k, kn = make(rng, (B, KH, L, E), dtype, dev)
@@ -183,14 +186,16 @@ def test_four_wave_dkdv_groups(dev, dt, causal):
     kpad[1, 256:384] = False
     kpad[2, -77:] = False
     kp = torch.from_numpy(kpad).to(dev)
-    print(f"four-wave dK/dV: {dt} (64,1024,16:8,4) causal={causal} key padding", flush=True)
+    print(f"four-wave groups: {dt} ({E},1024,16:{KH},4) causal={causal} key padding", flush=True)
     o, ms, ls = nnop._flash_attention(q, k, v, causal=causal, kpad_mask=kp)
     dq, dk, dv, _ = nnop.grad_flash_attention(do, o, ms, ls, q, k, v, causal=causal, kpad_mask=kp)
     torch.cuda.synchronize()
     scale = nnop.attention_scale(E, dtype)
     errs = {}
     for b in (1, 2):
-        sq, sk = (slice(b, b + 1), slice(10, 12)), (slice(b, b + 1), slice(5, 6))
+        rep = QH // KH
+        kvh = 10 // rep  # the kv head of q head 10, and all q heads of its group
+        sq, sk = (slice(b, b + 1), slice(kvh * rep, (kvh + 1) * rep)), (slice(b, b + 1), slice(kvh, kvh + 1))
         o_r, _, _ = oracle.attn_fwd(qn[sq], kn[sk], vn[sk], None, kpad[b:b + 1], causal, scale)
         dq_r, dk_r, dv_r, _ = oracle.attn_bwd(don[sq], qn[sq], kn[sk], vn[sk], None, kpad[b:b + 1], causal, scale)
         errs.update({f"o{b}": rel_err(host(o[sq]), o_r), f"dq{b}": rel_err(host(dq[sq]), dq_r),
