@@ -172,3 +172,39 @@ def test_varlen_errors(dev):
     with pytest.raises(ValueError, match="divisible"):
         nnop._flash_attention_varlen(torch.zeros((3, 10, 64), dtype=torch.bfloat16, device=dev), q, q, cu, cu,
                                      10, 10, causal=True)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_four_wave_groups(dev, causal):
+    """Packed sequences on a grid large enough for the four-wave forward and dQ groups at
+    E = 128 (at least 256 workgroups of 128 queries): bf16, 16:4 heads, lengths
+    [700, 1025, 300, 513].  Sequences and heads are independent, so sequences 1 and 3 of
+    kv head 1 (q heads 4..7) are exact sub-problems for the oracle."""
+    rng = np.random.default_rng(31)
+    E, QH, KH = 128, 16, 4
+    lens = [700, 1025, 300, 513]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    q, qn = make(rng, (QH, T, E), torch.bfloat16, dev)
+    k, kn = make(rng, (KH, T, E), torch.bfloat16, dev)
+    v, vn = make(rng, (KH, T, E), torch.bfloat16, dev)
+    do, don = make(rng, (QH, T, E), torch.bfloat16, dev)
+    cut = torch.from_numpy(cu).to(dev)
+    mx = max(lens)
+    print(f"varlen four-wave groups: bf16 E=128 16:4 lens={lens} causal={causal}", flush=True)
+    o, ms, ls = nnop._flash_attention_varlen(q, k, v, cut, cut, mx, mx, causal=causal)
+    dq, dk, dv = nnop.grad_flash_attention_varlen(do, o, ms, ls, q, k, v, cut, cut, mx, mx, causal=causal,
+                                                  qk_fp16=False)
+    torch.cuda.synchronize()
+    scale = nnop.attention_scale(E, torch.bfloat16)
+    o, dq, dk, dv = (host(t) for t in (o, dq, dk, dv))
+    errs = {}
+    for s in (1, 3):
+        a, b = cu[s], cu[s + 1]
+        sq = lambda x: x[4:8, a:b][None]
+        sk = lambda x: x[1:2, a:b][None]
+        o_r, _, _ = oracle.attn_fwd(sq(qn), sk(kn), sk(vn), None, None, causal, scale)
+        dq_r, dk_r, dv_r, _ = oracle.attn_bwd(sq(don), sq(qn), sk(kn), sk(vn), None, None, causal, scale)
+        errs.update({f"o{s}": rel_err(o[4:8, a:b], o_r[0]), f"dq{s}": rel_err(dq[4:8, a:b], dq_r[0]),
+                     f"dk{s}": rel_err(dk[1:2, a:b], dk_r[0]), f"dv{s}": rel_err(dv[1:2, a:b], dv_r[0])})
+    assert all(e <= TOL[torch.bfloat16] for e in errs.values()), errs
