@@ -369,6 +369,22 @@ __device__ __forceinline__ QBlock qblock_map(int x, int QH, int KH, int NB) {
     return r;
 }
 
+// (rank, batch, q head) of block x of a grid of n = nq NB QH blocks (nq ranks, nq % 4 == 0)
+// that is resident all at once, four blocks per CU, with blocks x, x + n/4, x + n/2 and
+// x + 3n/4 on one CU (the dispatcher fills the CUs round by round).  The plain order gives
+// CU c the ranks k, k + nq/4, k + nq/2, k + 3nq/4 (k = c / (NB QH)), whose causal work
+// falls with k; here the four slots take ranks k, nq/2 - 1 - k, nq/2 + k and nq - 1 - k,
+// whose work sums to the same for every CU, and the longest ranks still start first.
+__device__ __forceinline__ QBlock qblock_balanced(int x, int n, int nq, int QH, int NB) {
+    const int q4 = nq / 4, quarter = n / 4, slot = x / quarter, c = x % quarter;
+    const int BH = QH * NB, k = c / BH, bh = c % BH;
+    QBlock r;
+    r.rank = slot == 0 ? k : slot == 1 ? 2 * q4 - 1 - k : slot == 2 ? 2 * q4 + k : 4 * q4 - 1 - k;
+    r.b = bh / QH;
+    r.qh = bh % QH;
+    return r;
+}
+
 // Packed variable-length sequences: sequence b is rows cu_q[b] .. cu_q[b+1] of every q
 // head's (Tq x E) slab (and of the per-query statistics), rows cu_k[b] .. cu_k[b+1] of
 // every k / v head's (Tk x E) slab.  cu_q == nullptr: dense (B, H, L, E) tensors.

@@ -1,4 +1,6 @@
 // attn_dispatch.hip -- element-type dispatch of the attention launchers.
+#include <atomic>
+
 #include "launch.h"
 
 // float32 through bf16x6 MFMA products (attn_f32x6.hip)
@@ -28,6 +30,19 @@ static __global__ void zero_bytes_kernel(void* p, int64_t bytes) {
     unsigned char* c = reinterpret_cast<unsigned char*>(p);
     for (int j = 0; j < 4; ++j)
         if (i + j < bytes) c[i + j] = 0;
+}
+
+int device_cu_count() {
+    static std::atomic<int> cache[64];  // 0: not queried yet, -1: query failed
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        int n = 0;
+        v = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : -1;
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v > 0 ? v : 0;
 }
 
 bool launch_attn_fwd(hipStream_t s, int dt, const AttnArgs& a) {

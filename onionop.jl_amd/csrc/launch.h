@@ -58,6 +58,9 @@ bool launch_rope_table(hipStream_t s, int64_t dim, int64_t rows, float base, con
 bool launch_rope(hipStream_t s, int dt, int64_t E, int64_t L, int64_t QH, int64_t KH, int64_t B, const void* q,
                  const void* k, const float* cosv, const float* sinv, float sign, void* qo, void* ko);
 
+// Compute units of the current device (cached per device; 0 if the query fails).
+int device_cu_count();
+
 // Longest row (elements) the row-wise kernels keep in registers for dtype dt.
 int64_t max_row_elems(int dt);
 // Number of workgroups (= float32 partial rows in the workspace) of the norm backward.
