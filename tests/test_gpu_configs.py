@@ -212,3 +212,34 @@ def test_config5_rope_gqa_varlen(dev):
     rhs = don.reshape(B, KH, QH // KH, L, E).sum(axis=(2, 3))     # (B, KH, E)
     assert rel_err(lhs, rhs) <= 2e-2, rel_err(lhs, rhs)
     assert torch.isfinite(o).all() and torch.isfinite(dq).all()
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_long_sequence_causal(dev, dt):
+    """A 65536-token causal sequence (E = 64, 2 heads): large row and tile indices in every
+    kernel.  Under the causal mask the first 256 queries see only the first 256 keys, so
+    o and dq of those rows are an exact sub-problem for the oracle; for every head,
+    sum_k dV = sum_q dO (each causal row of P sums to one) checks the whole dV, and every
+    gradient is finite."""
+    dtype = {"bf16": torch.bfloat16, "f32": torch.float32}[dt]
+    B, H, L, E = 1, 2, 65536, 64
+    rng = np.random.default_rng(17)
+    s = 1.0 / np.sqrt(E)
+    q, qn = make(rng, (B, H, L, E), dtype, dev, scale=s)
+    k, kn = make(rng, (B, H, L, E), dtype, dev, scale=s)
+    v, vn = make(rng, (B, H, L, E), dtype, dev)
+    do, don = make(rng, (B, H, L, E), dtype, dev)
+    print(f"long sequence: {dt} (64, 65536, 2, 1) causal", flush=True)
+    o, ms, ls = nnop._flash_attention(q, k, v, causal=True)
+    dq, dk, dv, _ = nnop.grad_flash_attention(do, o, ms, ls, q, k, v, causal=True, qk_fp16=False)
+    torch.cuda.synchronize()
+    scale = nnop.attention_scale(E, dtype)
+    P = 256
+    o_r, _, _ = oracle.attn_fwd(qn[:, :, :P], kn[:, :, :P], vn[:, :, :P], causal=True, scale=scale)
+    dq_r, _, _, _ = oracle.attn_bwd(don[:, :, :P], qn[:, :, :P], kn[:, :, :P], vn[:, :, :P], causal=True, scale=scale)
+    errs = {"o[:256]": rel_err(host(o[:, :, :P]), o_r), "dq[:256]": rel_err(host(dq[:, :, :P]), dq_r)}
+    check(errs, TOL[dtype])
+    dvsum = host(dv).astype(np.float64).sum(axis=2)
+    dosum = host(do).astype(np.float64).sum(axis=2)
+    assert rel_err(dvsum, dosum) <= (2e-2 if dtype != torch.float32 else 1e-4), rel_err(dvsum, dosum)
+    assert torch.isfinite(dq).all() and torch.isfinite(dk).all() and torch.isfinite(dv).all()
