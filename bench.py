@@ -522,7 +522,6 @@ def counter_summary(paths, last=20):
       bank_conflict_share = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE
       valu_per_mfma = SQ_INSTS_VALU / SQ_INSTS_MFMA"""
     import csv
-    import re
 
     def short(mangled):  # last name of an Itanium nested name: _ZN7onionop20attn_fwd_pipe_kernelI...
         if not mangled.startswith("_ZN"):

@@ -6,7 +6,6 @@ launches (no memsets, allocations or synchronisations; zero fills are kernels), 
 replay must reproduce the eager results bit for bit.  Between replays the inputs are
 refilled by eager work and the process synchronises; every replay is checked.
 """
-import numpy as np
 import pytest
 import torch
 

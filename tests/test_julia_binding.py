@@ -11,8 +11,6 @@ import ctypes
 import os
 import re
 
-import pytest
-
 from nnop import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
