@@ -99,6 +99,37 @@ __device__ __forceinline__ void load_w(const void* __restrict__ w, int dt, int64
     }
 }
 
+// Dtype code of T (F32 = 0, F16 = 1, BF16 = 2), the codes of the weight dtype `dtw`.
+template <typename T>
+constexpr int dt_code() { return sizeof(T) == 4 ? 0 : __is_same(T, f16) ? 1 : 2; }
+
+// A norm's per-thread weights, held for the whole kernel.  PACKED (16-bit weights of the
+// row's own dtype in 16-byte slots) keeps the raw slots, half the registers of floats, and
+// widens them where used; otherwise floats of any weight dtype.
+template <typename T, int VEC, int NV, bool PACKED>
+struct RowWeights {
+    float v[NV][VEC];
+    __device__ __forceinline__ void load(const void* __restrict__ w, int dt, int64_t n) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) load_w<VEC>(w, dt, n, i, v[i]);
+    }
+    __device__ __forceinline__ void get(int i, float* out) const {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) out[j] = v[i][j];
+    }
+};
+template <typename T, int VEC, int NV>
+struct RowWeights<T, VEC, NV, true> {
+    static_assert(sizeof(T) == 2 && VEC != 1, "packed weights are 16-bit 16-byte slots");
+    typename RowIO<T, VEC>::raw v[NV];
+    __device__ __forceinline__ void load(const void* __restrict__ w, int, int64_t n) {
+        const rsrc_t r = make_rsrc(w, (uint32_t)(n * 2));  // slots past the end read 0
+#pragma unroll
+        for (int i = 0; i < NV; ++i) v[i] = bload16(r, RowIO<T, VEC>::off(i));
+    }
+    __device__ __forceinline__ void get(int i, float* out) const { RowIO<T, VEC>::to_float(v[i], out); }
+};
+
 // Rows handled together per loop iteration: short rows (NV < 4 vectors per thread) are
 // processed R at a time, which halves (or quarters) the barriers per row and keeps more
 // bytes in flight per thread.
@@ -334,9 +365,20 @@ __global__ __launch_bounds__(kThreads) void softmax_bwd2_kernel(const T* __restr
     }
 }
 
+// Marks raw row slots as rewritten (an empty asm), so that a second pass over them widens
+// them again instead of keeping the first pass's floats live across a reduction: the
+// floats of a 16-bit row take twice the registers of its raw slots.
+template <int R, int NV, typename Raw>
+__device__ __forceinline__ void reload_barrier(Raw (&a)[R][NV], Raw (&b)[R][NV]) {
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+        for (int i = 0; i < NV; ++i) asm volatile("" : "+v"(a[k][i]), "+v"(b[k][i]));
+}
+
 // ------------------------------------------------------------------ RMS norm
 // rstd = 1/sqrt(mean(x^2) + eps); y = (offset + w) x rstd (_rms_norm!, src/rms_norm.jl:3-38).
-template <typename T, int VEC, int NV, int D>
+template <typename T, int VEC, int NV, int D, bool PW>
 __global__ __launch_bounds__(kThreads) void rms_fwd_kernel(const T* __restrict__ x, const void* __restrict__ w, int dtw,
                                                             T* __restrict__ y, float* __restrict__ rstd,
                                                             int64_t n, int64_t rows, float eps, float offset) {
@@ -344,13 +386,8 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_kernel(const T* __restrict__
     constexpr int R = RowsPerIter<NV>::R;
     __shared__ float red[2 * kWaves * R];
     int par = 0;
-    float wv[NV][VEC];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        load_w<VEC>(w, dtw, n, i, wv[i]);
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) wv[i][j] += offset;
-    }
+    RowWeights<T, VEC, NV, PW> wv;
+    wv.load(w, dtw, n);
     const float inv_n = 1.0f / (float)n;
     const int64_t nblk = (rows + R - 1) / R;
     typename IO::raw buf[D][R][NV];
@@ -381,8 +418,10 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_kernel(const T* __restrict__
             const rsrc_t ry = row_rsrc(y, r, rows, n);
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
+                float wf[VEC];
+                wv.get(i, wf);
 #pragma unroll
-                for (int j = 0; j < VEC; ++j) v[k][i][j] = wv[i][j] * v[k][i][j] * rs;
+                for (int j = 0; j < VEC; ++j) v[k][i][j] = (wf[j] + offset) * v[k][i][j] * rs;
                 IO::store(ry, i, v[k][i]);
             }
         }
@@ -403,7 +442,7 @@ __device__ __forceinline__ void load_stats(const float* p, int64_t rb, int64_t r
 // Per row: dd = sum(dy (w+off) x); dx = rstd dy (w+off) - rstd^3 dd x / n; the dw partial
 // sum(dy x rstd) over this workgroup's rows goes to ws[blockIdx.x, :]
 // (_∇rms_norm!, src/rms_norm.jl:43-115).
-template <typename T, int VEC, int NV, int D>
+template <typename T, int VEC, int NV, int D, bool PW>
 __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__ dy, const float* __restrict__ rstd,
                                                             const T* __restrict__ x, const void* __restrict__ w, int dtw,
                                                             float offset, T* __restrict__ dx, float* __restrict__ ws,
@@ -412,13 +451,13 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
     constexpr int R = RowsPerIter<NV>::R;
     __shared__ float red[2 * kWaves * R];
     int par = 0;
-    float wv[NV][VEC], dw[NV][VEC];
+    RowWeights<T, VEC, NV, PW> wv;
+    wv.load(w, dtw, n);
+    float dw[NV][VEC];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        load_w<VEC>(w, dtw, n, i, wv[i]);
+    for (int i = 0; i < NV; ++i)
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) { wv[i][j] += offset; dw[i][j] = 0.f; }
-    }
+        for (int j = 0; j < VEC; ++j) dw[i][j] = 0.f;
     const float inv_n = 1.0f / (float)n;
     const int64_t nblk = (rows + R - 1) / R;
     typename IO::raw bg[D][R][NV], bx[D][R][NV];
@@ -432,14 +471,17 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
     }
     for_row_blocks<D>(nblk, [&](auto slot, int64_t rb) {
         constexpr int sl = decltype(slot)::value;
-        float g[R][NV][VEC], xv[R][NV][VEC], dd[R], crs[R];
+        // The current rows stay in their raw slots and are widened in each of the two
+        // passes (half the registers of floats for 16-bit rows).
+        typename IO::raw cg[R][NV], cx[R][NV];
+        float dd[R], crs[R];
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             crs[k] = brs[sl][k];
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                IO::to_float(bg[sl][k][i], g[k][i]);
-                IO::to_float(bx[sl][k][i], xv[k][i]);
+                cg[k][i] = bg[sl][k][i];
+                cx[k][i] = bx[sl][k][i];
             }
         }
         const int64_t nb = rb + (int64_t)D * gridDim.x;
@@ -450,11 +492,17 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
         for (int k = 0; k < R; ++k) {
             dd[k] = 0.f;
 #pragma unroll
-            for (int i = 0; i < NV; ++i)
+            for (int i = 0; i < NV; ++i) {
+                float g[VEC], xv[VEC], wf[VEC];
+                IO::to_float(cg[k][i], g);
+                IO::to_float(cx[k][i], xv);
+                wv.get(i, wf);
 #pragma unroll
-                for (int j = 0; j < VEC; ++j) dd[k] = fmaf(g[k][i][j] * wv[i][j], xv[k][i][j], dd[k]);
+                for (int j = 0; j < VEC; ++j) dd[k] = fmaf(g[j] * (wf[j] + offset), xv[j], dd[k]);
+            }
         }
         block_reduce_n<R, false>(dd, red, par);
+        reload_barrier<R, NV>(cg, cx);
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             const float rs = crs[k];  // 0 for rows past the end, whose g and x are 0 too
@@ -462,12 +510,16 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
             const rsrc_t rx = row_rsrc(dx, rb * R + k, rows, n);
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
+                float g[VEC], xv[VEC], wf[VEC];
+                IO::to_float(cg[k][i], g);
+                IO::to_float(cx[k][i], xv);
+                wv.get(i, wf);
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
-                    dw[i][j] = fmaf(g[k][i][j], xv[k][i][j] * rs, dw[i][j]);
-                    g[k][i][j] = rs * g[k][i][j] * wv[i][j] - c3 * xv[k][i][j];
+                    dw[i][j] = fmaf(g[j], xv[j] * rs, dw[i][j]);
+                    g[j] = rs * g[j] * (wf[j] + offset) - c3 * xv[j];
                 }
-                IO::store(rx, i, g[k][i]);
+                IO::store(rx, i, g);
             }
         }
     });
@@ -483,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_kernel(const T* __restrict__
 // ------------------------------------------------------------------ layer norm
 // mu = mean(x); rstd = 1/sqrt(mean((x-mu)^2) + eps); y = (x-mu) rstd w + b
 // (_layer_norm!, src/layer_norm.jl:8-63).
-template <typename T, int VEC, int NV, int D>
+template <typename T, int VEC, int NV, int D, bool PW>
 __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ x, const void* __restrict__ w,
                                                            const void* __restrict__ b, int dtw, T* __restrict__ y,
                                                            float* __restrict__ mu, float* __restrict__ rstd,
@@ -492,12 +544,9 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ 
     constexpr int R = RowsPerIter<NV>::R;
     __shared__ float red[2 * kWaves * R];
     int par = 0;
-    float wv[NV][VEC], bv[NV][VEC];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        load_w<VEC>(w, dtw, n, i, wv[i]);
-        load_w<VEC>(b, dtw, n, i, bv[i]);
-    }
+    RowWeights<T, VEC, NV, PW> wv, bv;
+    wv.load(w, dtw, n);
+    bv.load(b, dtw, n);
     const float inv_n = 1.0f / (float)n;
     const int64_t nblk = (rows + R - 1) / R;
     typename IO::raw buf[D][R][NV];
@@ -544,8 +593,11 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ 
             const rsrc_t ry = row_rsrc(y, r, rows, n);
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
+                float wf[VEC], bf[VEC];
+                wv.get(i, wf);
+                bv.get(i, bf);
 #pragma unroll
-                for (int j = 0; j < VEC; ++j) v[k][i][j] = fmaf((v[k][i][j] - m[k]) * rs, wv[i][j], bv[i][j]);
+                for (int j = 0; j < VEC; ++j) v[k][i][j] = fmaf((v[k][i][j] - m[k]) * rs, wf[j], bf[j]);
                 IO::store(ry, i, v[k][i]);
             }
         }
@@ -555,7 +607,7 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ 
 // Per row: xn = (x-mu) rstd; c1 = mean(w dy xn); c2 = mean(w dy);
 // dx = (w dy - (xn c1 + c2)) rstd; partials of dw = sum dy xn and db = sum dy go to
 // ws[blockIdx.x, :] and ws[grid + blockIdx.x, :] (_∇layer_norm!, src/layer_norm.jl:65-148).
-template <typename T, int VEC, int NV, int D>
+template <typename T, int VEC, int NV, int D, bool PW>
 __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ dy, const float* __restrict__ mu,
                                                            const float* __restrict__ rstd, const T* __restrict__ x,
                                                            const void* __restrict__ w, int dtw, T* __restrict__ dx,
@@ -564,13 +616,13 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
     constexpr int R = RowsPerIter<NV>::R;
     __shared__ float red[2 * kWaves * 2 * R];
     int par = 0;
-    float wv[NV][VEC], dw[NV][VEC], db[NV][VEC];
+    RowWeights<T, VEC, NV, PW> wv;
+    wv.load(w, dtw, n);
+    float dw[NV][VEC], db[NV][VEC];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        load_w<VEC>(w, dtw, n, i, wv[i]);
+    for (int i = 0; i < NV; ++i)
 #pragma unroll
         for (int j = 0; j < VEC; ++j) dw[i][j] = db[i][j] = 0.f;
-    }
     const float inv_n = 1.0f / (float)n;
     const int64_t nblk = (rows + R - 1) / R;
     typename IO::raw bg[D][R][NV], bx[D][R][NV];
@@ -585,17 +637,18 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
     }
     for_row_blocks<D>(nblk, [&](auto slot, int64_t rb) {
         constexpr int sl = decltype(slot)::value;
-        float g[R][NV][VEC], xv[R][NV][VEC], c12[2 * R], crs[R];
+        // The current rows stay in their raw slots (half the registers of floats for
+        // 16-bit rows) and are widened, xn = (x-mu) rstd too, in each of the two passes.
+        typename IO::raw cg[R][NV], cx[R][NV];
+        float c12[2 * R], cm[R], crs[R];
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-            const float cm = bm[sl][k];
+            cm[k] = bm[sl][k];
             crs[k] = brs[sl][k];
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                IO::to_float(bg[sl][k][i], g[k][i]);
-                IO::to_float(bx[sl][k][i], xv[k][i]);
-#pragma unroll
-                for (int j = 0; j < VEC; ++j) xv[k][i][j] = (xv[k][i][j] - cm) * crs[k];  // xn
+                cg[k][i] = bg[sl][k][i];
+                cx[k][i] = bx[sl][k][i];
             }
         }
         const int64_t nb = rb + (int64_t)D * gridDim.x;
@@ -603,31 +656,44 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
         load_rows<T, VEC, NV, R>(x, nb, rows, n, bx[sl]);
         load_stats<R>(mu, nb, rows, bm[sl]);
         load_stats<R>(rstd, nb, rows, brs[sl]);
+        auto widen = [&](int k, int i, float* g, float* xn) {
+            IO::to_float(cg[k][i], g);
+            IO::to_float(cx[k][i], xn);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) xn[j] = (xn[j] - cm[k]) * crs[k];
+        };
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             c12[2 * k] = c12[2 * k + 1] = 0.f;
 #pragma unroll
-            for (int i = 0; i < NV; ++i)
+            for (int i = 0; i < NV; ++i) {
+                float g[VEC], xn[VEC], wf[VEC];
+                widen(k, i, g, xn);
+                wv.get(i, wf);
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {  // zero-padded slots give g = 0
-                    const float wdy = wv[i][j] * g[k][i][j];
-                    c12[2 * k] = fmaf(wdy, xv[k][i][j], c12[2 * k]);
+                    const float wdy = wf[j] * g[j];
+                    c12[2 * k] = fmaf(wdy, xn[j], c12[2 * k]);
                     c12[2 * k + 1] += wdy;
                 }
+            }
         }
         block_reduce_n<2 * R, false>(c12, red, par);
+        reload_barrier<R, NV>(cg, cx);
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             const float c1 = c12[2 * k] * inv_n, c2 = c12[2 * k + 1] * inv_n, rs = crs[k];
             const rsrc_t rx = row_rsrc(dx, rb * R + k, rows, n);
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                float o[VEC];
+                float o[VEC], g[VEC], xn[VEC], wf[VEC];
+                widen(k, i, g, xn);
+                wv.get(i, wf);
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
-                    o[j] = (wv[i][j] * g[k][i][j] - fmaf(xv[k][i][j], c1, c2)) * rs;
-                    dw[i][j] = fmaf(g[k][i][j], xv[k][i][j], dw[i][j]);
-                    db[i][j] += g[k][i][j];
+                    o[j] = (wf[j] * g[j] - fmaf(xn[j], c1, c2)) * rs;
+                    dw[i][j] = fmaf(g[j], xn[j], dw[i][j]);
+                    db[i][j] += g[j];
                 }
                 IO::store(rx, i, o);
             }
@@ -794,14 +860,30 @@ struct SoftmaxBwd2 {
         return true;
     }
 };
+// Calls f(std::true_type) when a norm's weights (w, and b if not NULL) can be held packed:
+// 16-bit weights of the row's own dtype, read as 16-byte slots, so 16-byte aligned.
+// Else f(std::false_type).
+template <typename T, int VEC, typename F>
+static void with_weights(int dtw, const void* w, const void* b, F&& f) {
+    if constexpr (sizeof(T) == 2 && VEC != 1) {
+        if (dtw == dt_code<T>() && ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b)) & 15u) == 0) {
+            f(std::true_type());
+            return;
+        }
+    }
+    f(std::false_type());
+}
+
 template <typename T, int VEC, int NV>
 struct RmsFwd {
     static bool run(hipStream_t s, const void* x, const void* w, int dtw, void* y, float* rstd, int64_t n,
                     int64_t rows, float eps, float offset) {
-        const auto k = rms_fwd_kernel<T, VEC, NV, 1>;
-        static const int fit = fit_per_cu(k);
-        k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 1)), dim3(kThreads), 0, s>>>(
-            (const T*)x, w, dtw, (T*)y, rstd, n, rows, eps, offset);
+        with_weights<T, VEC>(dtw, w, nullptr, [&](auto pw) {
+            const auto k = rms_fwd_kernel<T, VEC, NV, 1, decltype(pw)::value>;
+            static const int fit = fit_per_cu(k);
+            k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 1)), dim3(kThreads), 0, s>>>(
+                (const T*)x, w, dtw, (T*)y, rstd, n, rows, eps, offset);
+        });
         return true;
     }
 };
@@ -809,8 +891,11 @@ template <typename T, int VEC, int NV>
 struct RmsBwd {
     static bool run(hipStream_t s, const void* dy, const float* rstd, const void* x, const void* w, int dtw,
                     float offset, void* dx, float* ws, int64_t groups, int64_t n, int64_t rows) {
-        rms_bwd_kernel<T, VEC, NV, BwdDepth<NV>::D><<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>(
-            (const T*)dy, rstd, (const T*)x, w, dtw, offset, (T*)dx, ws, n, rows);
+        with_weights<T, VEC>(dtw, w, nullptr, [&](auto pw) {
+            rms_bwd_kernel<T, VEC, NV, BwdDepth<NV>::D, decltype(pw)::value>
+                <<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>((const T*)dy, rstd, (const T*)x, w, dtw, offset,
+                                                                   (T*)dx, ws, n, rows);
+        });
         return true;
     }
 };
@@ -818,10 +903,12 @@ template <typename T, int VEC, int NV>
 struct LnFwd {
     static bool run(hipStream_t s, const void* x, const void* w, const void* b, int dtw, void* y, float* mu,
                     float* rstd, int64_t n, int64_t rows, float eps) {
-        const auto k = ln_fwd_kernel<T, VEC, NV, 1>;
-        static const int fit = fit_per_cu(k);
-        k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 1)), dim3(kThreads), 0, s>>>(
-            (const T*)x, w, b, dtw, (T*)y, mu, rstd, n, rows, eps);
+        with_weights<T, VEC>(dtw, w, b, [&](auto pw) {
+            const auto k = ln_fwd_kernel<T, VEC, NV, 1, decltype(pw)::value>;
+            static const int fit = fit_per_cu(k);
+            k<<<dim3(grid_blocks<T, NV>(fit, rows, n, 1)), dim3(kThreads), 0, s>>>(
+                (const T*)x, w, b, dtw, (T*)y, mu, rstd, n, rows, eps);
+        });
         return true;
     }
 };
@@ -829,8 +916,11 @@ template <typename T, int VEC, int NV>
 struct LnBwd {
     static bool run(hipStream_t s, const void* dy, const float* mu, const float* rstd, const void* x,
                     const void* w, int dtw, void* dx, float* ws, int64_t groups, int64_t n, int64_t rows) {
-        ln_bwd_kernel<T, VEC, NV, BwdDepth<NV>::D><<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>(
-            (const T*)dy, mu, rstd, (const T*)x, w, dtw, (T*)dx, ws, n, rows);
+        with_weights<T, VEC>(dtw, w, nullptr, [&](auto pw) {
+            ln_bwd_kernel<T, VEC, NV, BwdDepth<NV>::D, decltype(pw)::value>
+                <<<dim3((unsigned)groups), dim3(kThreads), 0, s>>>((const T*)dy, mu, rstd, (const T*)x, w, dtw,
+                                                                   (T*)dx, ws, n, rows);
+        });
         return true;
     }
 };

@@ -181,6 +181,52 @@ def test_layer_norm_16bit(dev, dt, emb, n):
           TOL[dtype])
 
 
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("emb,n", [(4096, 64), (1024, 300), (16384, 8), (520, 7)])
+def test_norm_weight_layouts(dev, dt, emb, n):
+    """16-bit weights of the rows' own dtype at a 16-byte aligned address are held packed in
+    registers; the same values at an unaligned address, or as float32, take the float
+    path.  The float32 arithmetic is the same, so the statistics agree bit for bit and the
+    16-bit outputs to one unit in the last place: the compiler may round an output once
+    from an exact fused multiply-add (v_fma_mixlo_f16) in one kernel variant and via
+    float32 in another."""
+    dtype = DTYPES[dt]
+    rng = np.random.default_rng(emb + 5 * n)
+    x, _ = make(rng, (n, emb), dtype, dev)
+    g, _ = make(rng, (n, emb), dtype, dev)
+    w, _ = make(rng, (emb,), dtype, dev, scale=0.02, offset=1.0)
+    b, _ = make(rng, (emb,), dtype, dev, scale=0.02)
+
+    def shifted(t):  # the same values 2 bytes past a 16-byte boundary
+        buf = torch.zeros(emb + 8, dtype=dtype, device=dev)
+        v = buf[1:emb + 1]
+        v.copy_(t)
+        assert v.data_ptr() % 16 == 2
+        return v
+
+    def ulps(a, c):  # largest distance in units in the last place (16-bit) or exact (float32)
+        if a.dtype == torch.float32:
+            return 0 if torch.equal(a, c) else float("inf")
+        ia, ic = a.view(torch.int16).int(), c.view(torch.int16).int()
+        ia = torch.where(ia < 0, -(ia & 0x7FFF), ia)  # sign-magnitude to a monotone integer
+        ic = torch.where(ic < 0, -(ic & 0x7FFF), ic)
+        return int((ia - ic).abs().max())
+
+    out = {}
+    for name, (wl, bl) in {"packed": (w, b), "unaligned": (shifted(w), shifted(b)),
+                           "float32": (w.float(), b.float())}.items():
+        y, mu, rstd = nnop._layer_norm(x, wl, bl)
+        dx, dw, db = nnop.grad_layer_norm(g, mu, rstd, x, wl)
+        ry, rr = nnop._rms_norm(x, wl, offset=0.5)
+        rdx, rdw = nnop.grad_rms_norm(g, rr, x, wl, offset=0.5)
+        out[name] = [y, mu, rstd, dx, dw.to(dtype), db.to(dtype), ry, rr, rdx, rdw.to(dtype)]
+    torch.cuda.synchronize()
+    names = ["y", "mu", "rstd", "dx", "dw", "db", "rms y", "rms rstd", "rms dx", "rms dw"]
+    for other in ("unaligned", "float32"):
+        d = {nm: ulps(a, c) for nm, a, c in zip(names, out["packed"], out[other])}
+        assert max(d.values()) <= 1, f"packed vs {other} weights: {d}"
+
+
 def test_norm_autograd(dev):
     rng = np.random.default_rng(2)
     x, xn = make(rng, (9, 300), torch.float32, dev)
