@@ -1,7 +1,7 @@
 """CPU oracle for NNop's fused-kernel hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py``
-may import this package, and only as the checker.  The product (``nnop`` and
+may import this package, and only to check results against.  The product (``nnop`` and
 ``libonionop_hip.so``) never calls it.
 
 Two layers:

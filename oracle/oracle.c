@@ -1,8 +1,9 @@
 /*
  * oracle.c -- CPU restatement of NNop's fused-kernel algorithms.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP library, never
- * part of it: only tests, the smoke check and bench.py's CPU-baseline leg load it.
+ * TEST INFRASTRUCTURE ONLY.  The HIP library's results are checked against this file,
+ * which is never part of the library: only tests, the smoke check and bench.py's
+ * CPU-baseline leg load it.
  *
  * Every array is column-major exactly like the reference's Julia arrays (first index
  * contiguous) and is passed as double.  Two arithmetic modes:
