@@ -57,7 +57,7 @@ enum onionop_status {
     ONIONOP_OK = 0,
     ONIONOP_E_SHAPE = -1,        /* shape / size mismatch (reference `error(...)`, `@assert`) */
     ONIONOP_E_DTYPE = -2,        /* unknown or unsupported element type                       */
-    ONIONOP_E_UNSUPPORTED = -3,  /* valid request this build has no kernel for (e.g. E=512)   */
+    ONIONOP_E_UNSUPPORTED = -3,  /* valid request the library has no kernel for (e.g. E=512) */
     ONIONOP_E_HIP = -4,          /* a HIP runtime call failed                                  */
     ONIONOP_E_NULL = -5,         /* a required pointer is NULL                                 */
     ONIONOP_E_WORKSPACE = -6     /* workspace missing or smaller than the *_workspace() size   */
@@ -92,7 +92,7 @@ int onionop_device_lds_bytes(int device, size_t* bytes_out /* host pointer */);
  * scale multiplies Q.K before the bias; the reference passes T(1/sqrt(E))
  * (src/attention.jl:166).  E must be a power of two in {16, 32, 64, 128, 256};
  * QH % KH == 0 (q head j uses kv head j / (QH/KH), src/attention.jl:36).
- * Limits of this build (ONIONOP_E_UNSUPPORTED beyond them): L * E * sizeof(T) < 2^31
+ * Limits of the library (ONIONOP_E_UNSUPPORTED beyond them): L * E * sizeof(T) < 2^31
  * bytes per (head, batch) slice of q/k/v, and with a bias 64 * QL * QH * sizeof(T) < 2^32
  * (the kernels address 64 key rows of one bias slice with 32-bit offsets).
  * Rows whose keys are all masked give o = 0, ms = -Inf, ls = 0 (the reference

@@ -47,7 +47,7 @@ const char* dt_name(int dt) {
 }
 
 // Shape checks of _flash_attention / ∇flash_attention (src/attention.jl:153-156,
-// src/attention_bwd.jl:224-227) plus what this build supports.
+// src/attention_bwd.jl:224-227) plus what the library supports.
 int check_attn(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B) {
     if (!valid_attn_dt(dtype)) return fail(ONIONOP_E_DTYPE, "flash_attention: unsupported element type code %d", dtype);
     if (E < 0 || QL < 0 || KL < 0 || QH < 0 || KH < 0 || B < 0)
