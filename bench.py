@@ -535,6 +535,7 @@ def counter_summary(paths, last=20):
             last = mangled[end:end + n]
             pos = end + n
         args = mangled[pos:].split("EEEv")[0] if pos < len(mangled) else ""
+        args = args[1:] if args.startswith("I") else args  # "I" opens the template arguments
         return f"{last}<{args}>" if args else last  # template arguments keep instantiations apart
 
     acc = {}
