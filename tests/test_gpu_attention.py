@@ -47,10 +47,21 @@ def run_case(dev, dt, E, QL, KL, QH, KH, B, causal, use_pair, use_kpad, seed, qk
     dq_r, dk_r, dv_r, dp_r = oracle.attn_bwd(don, qn, kn, vn, pairn, kpad, causal, scale,
                                             qk_fp16=qk16 and dtype == torch.float32)
     tol = TOL[dtype]
-    errs = {"o": rel_err(host(o), o_r), "dq": rel_err(host(dq), dq_r), "dk": rel_err(host(dk), dk_r),
+
+    def grad_err(a, r):
+        # When every row's softmax sees at most one key, dS = P (dP - delta) is exactly zero
+        # and so are dq, dk and dpair; the kernel's values are then the float round-off of
+        # dP - delta, bounded against dv, a gradient of the same magnitude that does not
+        # cancel.
+        nv = np.linalg.norm(dv_r)
+        if np.linalg.norm(r) == 0.0 and nv > 0.0:
+            return float(np.linalg.norm(np.asarray(a, dtype=np.float64)) / nv)
+        return rel_err(a, r)
+
+    errs = {"o": rel_err(host(o), o_r), "dq": grad_err(host(dq), dq_r), "dk": grad_err(host(dk), dk_r),
             "dv": rel_err(host(dv), dv_r)}
     if use_pair:
-        errs["dpair"] = rel_err(host(dpair), dp_r)
+        errs["dpair"] = grad_err(host(dpair), dp_r)
     fin = np.isfinite(ms_r)
     errs["ms"] = rel_err(host(ms)[fin], ms_r[fin]) if fin.any() else 0.0
     errs["ls"] = rel_err(host(ls), ls_r)
