@@ -105,7 +105,10 @@ int onionop_flash_attn_fwd(void* stream, int dtype,
                            int causal, float scale,
                            void* o, float* ms, float* ls);
 
-/* Bytes of workspace onionop_flash_attn_bwd needs for these sizes. */
+/* Bytes of workspace the backward entry points use for these sizes: the log-sum-exp and
+ * rowsum(dO o) of every query row, and, for a 16-bit call with a pair bias on a grid of
+ * fewer than 192 four-head workgroups, float32 partial dQ rows of a key-range split.  A
+ * workspace of only 8 bytes per query row plus 256 also works; the dQ then runs unsplit. */
 size_t onionop_flash_attn_bwd_workspace(int dtype, int64_t E, int64_t QL, int64_t KL,
                                         int64_t QH, int64_t KH, int64_t B);
 

@@ -159,12 +159,29 @@ int onionop_flash_attn_fwd(void* stream, int dtype, int64_t E, int64_t QL, int64
     return check_launch("flash_attention");
 }
 
-size_t onionop_flash_attn_bwd_workspace(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
-                                        int64_t B) {
-    (void)dtype; (void)E; (void)KL; (void)KH;
+// The part of the backward workspace every call needs: lse2 and delta per query row.
+static size_t bwd_ws_base(int64_t QL, int64_t QH, int64_t B) {
     if (QL <= 0 || QH <= 0 || B <= 0) return 0;
     const size_t rows = (size_t)QL * (size_t)QH * (size_t)B;
     return 2 * rows * sizeof(float) + 256;  // lse2 and delta, each 256-byte aligned
+}
+
+// Offset of the key-range split's partial dQ rows (256-byte aligned after delta) and the
+// bytes they take; 0 when the shape takes no split.
+static size_t bwd_ws_split_off(int64_t QL, int64_t QH, int64_t B) {
+    return ((2 * (size_t)QL * (size_t)QH * (size_t)B * sizeof(float)) + 255) & ~size_t(255);
+}
+static size_t bwd_ws_split_bytes(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t B) {
+    const int n = onionop::dq_key_splits(dtype, E, QL, KL, QH, B);
+    return n > 1 ? (size_t)n * (size_t)QL * (size_t)QH * (size_t)B * (size_t)E * sizeof(float) : 0;
+}
+
+size_t onionop_flash_attn_bwd_workspace(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
+                                        int64_t B) {
+    (void)KH;
+    const size_t base = bwd_ws_base(QL, QH, B);
+    const size_t split = base > 0 ? bwd_ws_split_bytes(dtype, E, QL, KL, QH, B) : 0;
+    return split > 0 ? 256 + bwd_ws_split_off(QL, QH, B) + split : base;
 }
 
 // Shared body of the backward entry points; `stages` selects which kernels run.
@@ -198,9 +215,12 @@ static int attn_bwd_common(const char* what, int stages, void* stream, int dtype
         if (any_q && !dq) return fail(ONIONOP_E_NULL, "%s: NULL tensor pointer", what);
         if (!aligned16(dq)) return fail(ONIONOP_E_SHAPE, "%s: tensors must be 16-byte aligned", what);
     }
-    const size_t need = onionop_flash_attn_bwd_workspace(dtype, E, QL, KL, QH, KH, B);
+    // Calls need the lse2 / delta rows; the dQ of a pair-biased small grid uses the rest of
+    // the full size for its key-range split when it is given (else it runs unsplit).
+    const size_t need = bwd_ws_base(QL, QH, B);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-        return fail(ONIONOP_E_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", what, need, workspace_bytes);
+        return fail(ONIONOP_E_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", what,
+                    onionop_flash_attn_bwd_workspace(dtype, E, QL, KL, QH, KH, B), workspace_bytes);
     onionop::AttnArgs a{};
     a.E = E; a.QL = QL; a.KL = KL; a.QH = QH; a.KH = KH; a.B = B;
     a.q = q; a.k = k; a.v = v; a.pair = pair; a.kpad = kpad; a.causal = causal != 0; a.scale = scale;
@@ -220,6 +240,14 @@ static int attn_bwd_common(const char* what, int stages, void* stream, int dtype
         const size_t rows = (size_t)QL * (size_t)QH * (size_t)B;
         a.lse2 = reinterpret_cast<float*>(base);
         a.delta = a.lse2 + rows;
+        const size_t split = pair != nullptr && (stages & onionop::kBwdDq) && rope_cos == nullptr
+                                 ? bwd_ws_split_bytes(dtype, E, QL, KL, QH, B)
+                                 : 0;
+        const size_t off = bwd_ws_split_off(QL, QH, B);
+        if (split > 0 && (base - reinterpret_cast<uintptr_t>(workspace)) + off + split <= workspace_bytes) {
+            a.dq_part = reinterpret_cast<float*>(base + off);
+            a.dq_splits = onionop::dq_key_splits(dtype, E, QL, KL, QH, B);
+        }
     }
     if (!onionop::launch_attn_bwd((hipStream_t)stream, dtype, a, stages))
         return fail(ONIONOP_E_UNSUPPORTED, "%s: no kernel for %s E=%lld", what, dt_name(dtype), (long long)E);
@@ -255,7 +283,7 @@ int onionop_flash_attn_bwd_noalloc(void* stream, int dtype, int64_t E, int64_t Q
     const char* what = "∇flash_attention (no allocation)";
     int st = check_attn(dtype, E, QL, KL, QH, KH, B);
     if (st) return st;
-    const size_t need = onionop_flash_attn_bwd_workspace(dtype, E, QL, KL, QH, KH, B);
+    const size_t need = bwd_ws_base(QL, QH, B);  // the key-range split is used when it fits too
     if (need > kScratchBytes)
         return fail(ONIONOP_E_UNSUPPORTED,
                     "%s: needs %zu bytes of scratch (8 per query row), the library holds %zu "

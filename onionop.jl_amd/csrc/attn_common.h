@@ -466,6 +466,14 @@ struct RopeTab {
     int64_t rows;
 };
 
+// Key ranges of the four-head bias dQ spread over n workgroups each (n > 1): workgroup
+// range r writes its float32 partial dQ rows to part[r][row][E] (rows in dq's order), and
+// a second launch sums the n partials in range order into dq.  n <= 1: dQ directly.
+struct DqSplit {
+    float* part;
+    int n;
+};
+
 // Element type helpers for the float16-rounded Q/K of the reference backward.
 template <typename T, bool QK16>
 __device__ __forceinline__ T qk_round(T x) {

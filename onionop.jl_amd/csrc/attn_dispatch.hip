@@ -32,6 +32,17 @@ static __global__ void zero_bytes_kernel(void* p, int64_t bytes) {
         if (i + j < bytes) c[i + j] = 0;
 }
 
+int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t B) {
+    if ((dt != 1 && dt != 2) || E > 64 || QH % 4 != 0 || QL <= 0 || KL <= 0 || B <= 0) return 1;
+    const int64_t nwg4 = ((QL + 63) / 64) * (QH / 4) * B;
+    if (nwg4 >= 192) return 1;  // the unsplit four-head grid already fills the chip
+    int64_t n = 256 / nwg4;
+    const int64_t tiles2 = ((KL + 31) / 32) / 2;
+    if (n > 8) n = 8;
+    if (n > tiles2) n = tiles2;
+    return n > 1 ? (int)n : 1;
+}
+
 int device_cu_count() {
     static std::atomic<int> cache[64];  // 0: not queried yet, -1: query failed
     int dev = 0;

@@ -34,6 +34,10 @@ struct AttnArgs {
     // (QH, Tq, E) / (KH, Tk, E), statistics (QH, Tq), and cu_q / cu_k hold B + 1 offsets.
     const int *cu_q = nullptr, *cu_k = nullptr;
     int64_t Tq = 0, Tk = 0;
+    // Key-range split of the four-head bias dQ (dq_splits > 1): float32 partial rows in
+    // the workspace, dq_splits x (B, QH, QL, E).
+    float* dq_part = nullptr;
+    int dq_splits = 1;
 };
 
 bool launch_attn_fwd(hipStream_t s, int dt, const AttnArgs& a);
@@ -60,6 +64,10 @@ bool launch_rope(hipStream_t s, int dt, int64_t E, int64_t L, int64_t QH, int64_
 
 // Compute units of the current device (cached per device; 0 if the query fails).
 int device_cu_count();
+// Key ranges the dQ of a 16-bit pair-biased call spreads over (1: none), a function of the
+// shape only: four-head workgroups on a grid of fewer than 192 of them take enough ranges
+// to make about 256 workgroups, at most 8, each of at least two 32-key tiles.
+int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t B);
 
 // Longest row (elements) the row-wise kernels keep in registers for dtype dt.
 int64_t max_row_elems(int dt);

@@ -310,6 +310,68 @@ def test_staged_backward_matches_combined(dev, dt, E, L, QH, KH, causal, use_pai
     assert all(e <= tol for e in errs.values()), errs
 
 
+@pytest.mark.parametrize("dt,E,L,QH,KH,B,causal,use_kpad", [
+    ("bf16", 32, 768, 8, 8, 2, False, False),   # config 4's shape: 5 key ranges
+    ("f16", 64, 300, 4, 2, 1, True, True),      # GQA, causal, key padding, ragged: 5 ranges
+    ("bf16", 16, 130, 8, 4, 1, False, False),   # E = 16, short keys: 2 ranges
+])
+def test_pair_dq_key_split(dev, dt, E, L, QH, KH, B, causal, use_kpad):
+    """The dQ of a 16-bit pair-biased call on a small grid splits its key range over
+    several four-head workgroups and sums their float32 partials in range order when the
+    workspace has the full size onionop_flash_attn_bwd_workspace reports, and runs
+    unsplit with only the lse / delta part.  Both agree with the oracle; dk and dv do not
+    depend on the split (bit-equal), dq only through its summation order, and dpair = dS
+    only through its rounding: the two dQ kernels (four heads per workgroup or one) may
+    round an element of float16 dS once from an exact fused multiply-add or via float32
+    (one unit in the last place)."""
+    from nnop import _lib
+    from nnop._util import ptr
+
+    dtype = DTYPES[dt]
+    rng = np.random.default_rng(11)
+    q, qn = make(rng, (B, QH, L, E), dtype, dev)
+    k, kn = make(rng, (B, KH, L, E), dtype, dev)
+    v, vn = make(rng, (B, KH, L, E), dtype, dev)
+    do, don = make(rng, (B, QH, L, E), dtype, dev)
+    pair, pairn = make(rng, (B, L, L, QH), dtype, dev)
+    kpad = kp = None
+    if use_kpad:
+        kpad = np.ones((B, L), dtype=bool)
+        kpad[-1, -11:] = False
+        kp = torch.from_numpy(kpad).to(dev)
+    print(f"dq key split: {dt} E={E} L={L} QH={QH} KH={KH} B={B} causal={causal} kpad={use_kpad}", flush=True)
+    o, ms, ls = nnop._flash_attention(q, k, v, pair, causal=causal, kpad_mask=kp)
+    L_ = _lib.lib()
+    dtc = {torch.float16: 1, torch.bfloat16: 2}[dtype]
+    dims = (E, L, L, QH, KH, B)
+    full = int(L_.onionop_flash_attn_bwd_workspace(dtc, *dims))
+    base = 2 * B * QH * L * 4 + 256  # the lse2 / delta rows alone
+    assert full > base, (full, base)
+    s = torch.cuda.current_stream().cuda_stream
+    sc = nnop.attention_scale(E, dtype)
+    outs = {}
+    for name, wsb in (("split", full), ("unsplit", base)):
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        g = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(pair)]
+        _lib.check(L_.onionop_flash_attn_bwd(s, dtc, *dims, ptr(do), ptr(o), ptr(ms), ptr(ls), ptr(q), ptr(k),
+                                             ptr(v), ptr(pair), ptr(kp), int(causal), sc, 1, ptr(g[0]), ptr(g[1]),
+                                             ptr(g[2]), ptr(g[3]), ptr(ws), wsb))
+        outs[name] = g
+    torch.cuda.synchronize()
+    a, b = outs["split"], outs["unsplit"]
+    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2]), "dk / dv"
+    ia, ib = a[3].view(torch.int16).int(), b[3].view(torch.int16).int()
+    ia = torch.where(ia < 0, -(ia & 0x7FFF), ia)  # sign-magnitude to a monotone integer
+    ib = torch.where(ib < 0, -(ib & 0x7FFF), ib)
+    assert int((ia - ib).abs().max()) <= 1, "dpair beyond one unit in the last place"
+    assert rel_err(host(a[0]), host(b[0])) <= 1e-2
+    dq_r, dk_r, dv_r, dp_r = oracle.attn_bwd(don, qn, kn, vn, pairn, kpad, causal, sc)
+    for name, g in outs.items():
+        errs = {"dq": rel_err(host(g[0]), dq_r), "dk": rel_err(host(g[1]), dk_r), "dv": rel_err(host(g[2]), dv_r),
+                "dpair": rel_err(host(g[3]), dp_r)}
+        assert all(e <= TOL[dtype] for e in errs.values()), (name, errs)
+
+
 def test_shared_memory_query(dev):
     """NNop.shared_memory (src/NNop.jl:27-30, ext/NNopAMDGPUExt.jl:6-9): the LDS bytes per
     workgroup of the device, as hipDeviceProp_t.sharedMemPerBlock reports it (torch reads
