@@ -166,22 +166,33 @@ static size_t bwd_ws_base(int64_t QL, int64_t QH, int64_t B) {
     return 2 * rows * sizeof(float) + 256;  // lse2 and delta, each 256-byte aligned
 }
 
-// Offset of the key-range split's partial dQ rows (256-byte aligned after delta) and the
-// bytes they take; 0 when the shape takes no split.
-static size_t bwd_ws_split_off(int64_t QL, int64_t QH, int64_t B) {
-    return ((2 * (size_t)QL * (size_t)QH * (size_t)B * sizeof(float)) + 255) & ~size_t(255);
-}
-static size_t bwd_ws_split_bytes(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t B) {
-    const int n = onionop::dq_key_splits(dtype, E, QL, KL, QH, B);
-    return n > 1 ? (size_t)n * (size_t)QL * (size_t)QH * (size_t)B * (size_t)E * sizeof(float) : 0;
+// Layout of the range splits' partial rows after lse2 / delta (offsets from the 256-byte
+// aligned start, each 256-byte aligned): the dQ key ranges' rows, then the dK / dV query
+// ranges' rows; bytes 0 where a shape takes no split.
+struct BwdSplitLayout {
+    size_t dq_off, dq_bytes, kv_off, kv_bytes;
+};
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+static BwdSplitLayout bwd_split_layout(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
+                                       int64_t B) {
+    BwdSplitLayout l{};
+    if (QL <= 0 || QH <= 0 || B <= 0) return l;
+    const size_t rows = (size_t)QL * (size_t)QH * (size_t)B, rows_k = (size_t)KL * (size_t)KH * (size_t)B;
+    const int nq = onionop::dq_key_splits(dtype, E, QL, KL, QH, B);
+    const int nk = onionop::kv_query_splits(dtype, E, QL, KL, QH, KH, B);
+    l.dq_off = align256(2 * rows * sizeof(float));
+    l.dq_bytes = nq > 1 ? (size_t)nq * rows * (size_t)E * sizeof(float) : 0;
+    l.kv_off = align256(l.dq_off + l.dq_bytes);
+    l.kv_bytes = nk > 1 ? 2 * (size_t)nk * rows_k * (size_t)E * sizeof(float) : 0;
+    return l;
 }
 
 size_t onionop_flash_attn_bwd_workspace(int dtype, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH,
                                         int64_t B) {
-    (void)KH;
     const size_t base = bwd_ws_base(QL, QH, B);
-    const size_t split = base > 0 ? bwd_ws_split_bytes(dtype, E, QL, KL, QH, B) : 0;
-    return split > 0 ? 256 + bwd_ws_split_off(QL, QH, B) + split : base;
+    const BwdSplitLayout l = bwd_split_layout(dtype, E, QL, KL, QH, KH, B);
+    if (base == 0 || (l.dq_bytes == 0 && l.kv_bytes == 0)) return base;
+    return 256 + (l.kv_bytes > 0 ? l.kv_off + l.kv_bytes : l.dq_off + l.dq_bytes);
 }
 
 // Shared body of the backward entry points; `stages` selects which kernels run.
@@ -240,13 +251,18 @@ static int attn_bwd_common(const char* what, int stages, void* stream, int dtype
         const size_t rows = (size_t)QL * (size_t)QH * (size_t)B;
         a.lse2 = reinterpret_cast<float*>(base);
         a.delta = a.lse2 + rows;
-        const size_t split = pair != nullptr && (stages & onionop::kBwdDq) && rope_cos == nullptr
-                                 ? bwd_ws_split_bytes(dtype, E, QL, KL, QH, B)
-                                 : 0;
-        const size_t off = bwd_ws_split_off(QL, QH, B);
-        if (split > 0 && (base - reinterpret_cast<uintptr_t>(workspace)) + off + split <= workspace_bytes) {
-            a.dq_part = reinterpret_cast<float*>(base + off);
-            a.dq_splits = onionop::dq_key_splits(dtype, E, QL, KL, QH, B);
+        // The range splits of the pair-biased kernels, each where the workspace holds it.
+        if (pair != nullptr && rope_cos == nullptr) {
+            const BwdSplitLayout l = bwd_split_layout(dtype, E, QL, KL, QH, KH, B);
+            const size_t lead = base - reinterpret_cast<uintptr_t>(workspace);
+            if ((stages & onionop::kBwdDq) && l.dq_bytes > 0 && lead + l.dq_off + l.dq_bytes <= workspace_bytes) {
+                a.dq_part = reinterpret_cast<float*>(base + l.dq_off);
+                a.dq_splits = onionop::dq_key_splits(dtype, E, QL, KL, QH, B);
+            }
+            if ((stages & onionop::kBwdDkDv) && l.kv_bytes > 0 && lead + l.kv_off + l.kv_bytes <= workspace_bytes) {
+                a.kv_part = reinterpret_cast<float*>(base + l.kv_off);
+                a.kv_splits = onionop::kv_query_splits(dtype, E, QL, KL, QH, KH, B);
+            }
         }
     }
     if (!onionop::launch_attn_bwd((hipStream_t)stream, dtype, a, stages))

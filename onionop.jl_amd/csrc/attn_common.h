@@ -466,10 +466,11 @@ struct RopeTab {
     int64_t rows;
 };
 
-// Key ranges of the four-head bias dQ spread over n workgroups each (n > 1): workgroup
-// range r writes its float32 partial dQ rows to part[r][row][E] (rows in dq's order), and
-// a second launch sums the n partials in range order into dq.  n <= 1: dQ directly.
-struct DqSplit {
+// The reduction range of a four-head bias kernel spread over n workgroups (n > 1): keys
+// for dQ, queries for dK / dV.  Range r writes float32 partial rows to part[r][row][E]
+// (rows in the output's order; dK / dV: the n dK partials, then the n dV partials), and a
+// second launch sums the n partials in range order into the outputs.  n <= 1: direct.
+struct RangeSplit {
     float* part;
     int n;
 };

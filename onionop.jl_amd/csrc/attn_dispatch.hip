@@ -43,6 +43,18 @@ int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t
     return n > 1 ? (int)n : 1;
 }
 
+int kv_query_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B) {
+    if ((dt != 1 && dt != 2) || E > 64 || QH != KH || KH % 4 != 0 || QL <= 0 || KL <= 0 || B <= 0) return 1;
+    const int64_t nwg4 = ((KL + 63) / 64) * (KH / 4) * B;
+    if (nwg4 >= 192) return 1;
+    const int64_t bq = E >= 64 ? 32 : 64;  // the bias kernel's query tile
+    int64_t n = 256 / nwg4;
+    const int64_t tiles2 = ((QL + bq - 1) / bq) / 2;
+    if (n > 8) n = 8;
+    if (n > tiles2) n = tiles2;
+    return n > 1 ? (int)n : 1;
+}
+
 int device_cu_count() {
     static std::atomic<int> cache[64];  // 0: not queried yet, -1: query failed
     int dev = 0;

@@ -311,19 +311,20 @@ def test_staged_backward_matches_combined(dev, dt, E, L, QH, KH, causal, use_pai
 
 
 @pytest.mark.parametrize("dt,E,L,QH,KH,B,causal,use_kpad", [
-    ("bf16", 32, 768, 8, 8, 2, False, False),   # config 4's shape: 5 key ranges
-    ("f16", 64, 300, 4, 2, 1, True, True),      # GQA, causal, key padding, ragged: 5 ranges
-    ("bf16", 16, 130, 8, 4, 1, False, False),   # E = 16, short keys: 2 ranges
+    ("bf16", 32, 768, 8, 8, 2, False, False),   # config 4's shape: 5 key and 5 query ranges
+    ("f16", 64, 300, 4, 2, 1, True, True),      # GQA (dQ split only), causal, key padding
+    ("f16", 64, 300, 4, 4, 1, True, True),      # both splits, causal, key padding, ragged
+    ("bf16", 16, 130, 8, 4, 1, False, False),   # E = 16, short keys: 2 key ranges
 ])
-def test_pair_dq_key_split(dev, dt, E, L, QH, KH, B, causal, use_kpad):
-    """The dQ of a 16-bit pair-biased call on a small grid splits its key range over
-    several four-head workgroups and sums their float32 partials in range order when the
-    workspace has the full size onionop_flash_attn_bwd_workspace reports, and runs
-    unsplit with only the lse / delta part.  Both agree with the oracle; dk and dv do not
-    depend on the split (bit-equal), dq only through its summation order, and dpair = dS
-    only through its rounding: the two dQ kernels (four heads per workgroup or one) may
-    round an element of float16 dS once from an exact fused multiply-add or via float32
-    (one unit in the last place)."""
+def test_pair_range_splits(dev, dt, E, L, QH, KH, B, causal, use_kpad):
+    """On small grids, a 16-bit pair-biased backward splits the dQ's key range (and, with
+    QH = KH, the dK / dV's query range) over several four-head workgroups and sums their
+    float32 partials in range order, when the workspace has the full size
+    onionop_flash_attn_bwd_workspace reports; with only the lse / delta part it runs
+    unsplit.  Both agree with the oracle; dq, dk and dv differ only in summation order,
+    and dpair = dS only in its rounding: the two dQ kernels (four heads per workgroup or
+    one) may round an element of float16 dS once from an exact fused multiply-add or via
+    float32 (one unit in the last place)."""
     from nnop import _lib
     from nnop._util import ptr
 
@@ -359,7 +360,8 @@ def test_pair_dq_key_split(dev, dt, E, L, QH, KH, B, causal, use_kpad):
         outs[name] = g
     torch.cuda.synchronize()
     a, b = outs["split"], outs["unsplit"]
-    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2]), "dk / dv"
+    for j in (1, 2):  # dk, dv
+        assert rel_err(host(a[j]), host(b[j])) <= 1e-2
     ia, ib = a[3].view(torch.int16).int(), b[3].view(torch.int16).int()
     ia = torch.where(ia < 0, -(ia & 0x7FFF), ia)  # sign-magnitude to a monotone integer
     ib = torch.where(ib < 0, -(ib & 0x7FFF), ib)
