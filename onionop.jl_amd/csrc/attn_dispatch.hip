@@ -32,15 +32,22 @@ static __global__ void zero_bytes_kernel(void* p, int64_t bytes) {
         if (i + j < bytes) c[i + j] = 0;
 }
 
+// Ranges of `tiles` tiles: at most `want` and 8, each of at least two tiles, and no empty
+// one (ranges are runs of ceil(tiles / n) tiles).
+static int split_count(int64_t want, int64_t tiles) {
+    int64_t n = want < 8 ? want : 8;
+    if (n > tiles / 2) n = tiles / 2;
+    if (n <= 1) return 1;
+    const int64_t per = (tiles + n - 1) / n;
+    return (int)((tiles + per - 1) / per);
+}
+
 int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t B) {
     if ((dt != 1 && dt != 2) || E > 64 || QH % 4 != 0 || QL <= 0 || KL <= 0 || B <= 0) return 1;
     const int64_t nwg4 = ((QL + 63) / 64) * (QH / 4) * B;
     if (nwg4 >= 192) return 1;  // the unsplit four-head grid already fills the chip
-    int64_t n = 256 / nwg4;
-    const int64_t tiles2 = ((KL + 31) / 32) / 2;
-    if (n > 8) n = 8;
-    if (n > tiles2) n = tiles2;
-    return n > 1 ? (int)n : 1;
+    const int64_t tiles = (KL + 31) / 32;
+    return split_count(256 / nwg4, tiles);
 }
 
 int kv_query_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B) {
@@ -48,11 +55,7 @@ int kv_query_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64
     const int64_t nwg4 = ((KL + 63) / 64) * (KH / 4) * B;
     if (nwg4 >= 192) return 1;
     const int64_t bq = E >= 64 ? 32 : 64;  // the bias kernel's query tile
-    int64_t n = 256 / nwg4;
-    const int64_t tiles2 = ((QL + bq - 1) / bq) / 2;
-    if (n > 8) n = 8;
-    if (n > tiles2) n = tiles2;
-    return n > 1 ? (int)n : 1;
+    return split_count(256 / nwg4, (QL + bq - 1) / bq);
 }
 
 int device_cu_count() {
