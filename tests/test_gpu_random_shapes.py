@@ -2,8 +2,8 @@
 fixed sweeps do not list: lengths at and around the 32 / 64 / 128-row tile edges (and 1),
 query and key lengths that differ, GQA ratios, random key-padding masks (including a
 batch whose keys are all masked), pair bias, causal, Float16 Q/K in the float32
-backward, float32 through bf16x6 products, E = 256, and packed sequences with empty
-ones.  Every case prints its parameters before it runs.  Tolerance as everywhere: 1e-5 (float32), 2e-2 (16-bit) norm-wise relative
+backward, float32 through bf16x6 products, E = 256, pair-biased calls on grids small
+enough for the backward's range splits, and packed sequences with empty ones.  Every case prints its parameters before it runs.  Tolerance as everywhere: 1e-5 (float32), 2e-2 (16-bit) norm-wise relative
 error against the float64 oracle.
 """
 import contextlib
@@ -56,6 +56,33 @@ def test_random_dense(dev, case):
     with mode:
         run_case(dev, "f32" if dt == "f32x6" else dt, E, QL, KL, QH, KH, B, causal, pair, kpad is not None, seed,
                  qk16=qk16, kpad=kpad)
+
+
+def split_case(i):
+    """16-bit pair-biased calls on small grids, where the dQ splits its key range and, with
+    QH = KH, the dK / dV their query range over several four-head workgroups."""
+    rng = np.random.default_rng(4000 + i)
+    dt = ["f16", "bf16"][i % 2]
+    E = int(rng.choice([16, 32, 64]))
+    QH = int(rng.choice([4, 8]))
+    KH = QH if rng.random() < 0.7 else QH // 2
+    B = int(rng.choice([1, 2]))
+    QL, KL = length(rng) + 64, length(rng) + 64  # at least four 32-key tiles: two ranges
+    causal = bool(rng.random() < 0.4)
+    kpad = None
+    if rng.random() < 0.4:
+        kpad = rng.random((B, KL)) < 0.85
+    return dt, E, QL, KL, QH, KH, B, causal, True, kpad, 4000 + i, False
+
+
+SPLITS = [split_case(i) for i in range(24)]
+
+
+@pytest.mark.parametrize("case", SPLITS, ids=lambda c: "{}-E{}-{}x{}-h{}:{}-b{}{}{}".format(
+    c[0], c[1], c[2], c[3], c[4], c[5], c[6], "-causal" if c[7] else "", "-kpad" if c[9] is not None else ""))
+def test_random_pair_splits(dev, case):
+    dt, E, QL, KL, QH, KH, B, causal, pair, kpad, seed, qk16 = case
+    run_case(dev, dt, E, QL, KL, QH, KH, B, causal, pair, kpad is not None, seed, qk16=qk16, kpad=kpad)
 
 
 def varlen_case(i):
