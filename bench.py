@@ -510,6 +510,37 @@ def workloads(torch, nnop, dev):
     return out
 
 
+SWEEP = [  # (E, L, H, KH, B, causal): bf16 attention fwd+bwd shapes around the headline
+    (64, 1024, 16, 16, 4, True), (64, 2048, 8, 8, 4, True), (64, 4096, 4, 4, 4, True), (64, 8192, 4, 4, 2, True),
+    (64, 16384, 4, 4, 1, True), (64, 4096, 4, 4, 4, False), (64, 4096, 16, 4, 4, True), (64, 4096, 16, 16, 4, True),
+    (128, 1024, 16, 16, 4, True), (128, 4096, 4, 4, 4, True), (128, 4096, 32, 8, 1, True),
+    (128, 8192, 8, 2, 2, True), (128, 4096, 4, 4, 4, False), (32, 4096, 8, 8, 4, True), (16, 4096, 8, 8, 4, True),
+    (256, 2048, 4, 4, 2, True),
+]
+
+
+def sweep(torch, nnop, dev):
+    """bf16 flash attention fwd+bwd over SWEEP's shapes (q, k, v ~ N(0,1)/sqrt(E), dO = 1),
+    timed as the headline: settled clocks, then HIP events; FLOPs 14 B H L^2 E (x 1/2 causal)."""
+    out = []
+    for E, L, H, KH, B, causal in SWEEP:
+        g = torch.Generator(device="cpu").manual_seed(5)
+        s = 1.0 / math.sqrt(E)
+        q = (torch.randn((B, H, L, E), generator=g) * s).to(torch.bfloat16).to(dev)
+        k, v = [(torch.randn((B, KH, L, E), generator=g) * s).to(torch.bfloat16).to(dev) for _ in range(2)]
+        do = torch.ones_like(q)
+        st = AttnStep(torch, nnop, q, k, v, do, causal=causal)
+        fl = 14 * B * H * L * L * E / (2 if causal else 1)
+        settle(torch, st.step, min_ms=60.0, max_ms=300.0, chunk=5)
+        t = time_region(torch, st.step, 20) * 1e3
+        rec = {"E": E, "L": L, "H": H, "KH": KH, "B": B, "causal": causal, "us": round(t, 1),
+               "TFLOP/s": round(fl / t / 1e6, 1), "frac_of_bf16_mfma": round(fl / t / 1e6 / MI355X_BF16_DENSE_TFLOPS, 3)}
+        log(f"  sweep {rec}")
+        out.append(rec)
+        del q, k, v, do, st
+    return out
+
+
 def counter_summary(paths, last=20):
     """Per-kernel averages of rocprofv3 --pmc counter CSVs (the last `last` dispatches of each
     kernel, i.e. the timed steps), with the derived utilisations:
@@ -581,6 +612,9 @@ def main():
     ap.add_argument("--workloads", action="store_true",
                     help="only time the other attention workloads (float32, pair bias, RoPE + GQA key mask "
                          "and packed) and print them as one JSON line")
+    ap.add_argument("--sweep", action="store_true",
+                    help="only time bf16 attention fwd+bwd over a list of shapes around the headline "
+                         "and print them as one JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run 3 plain device copies of MIB MiB (a known-size kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -601,6 +635,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.workloads:
         print(json.dumps(workloads(torch, nnop, dev)), flush=True)
+        return
+    if args.sweep:
+        print(json.dumps({"sweep": sweep(torch, nnop, dev)}), flush=True)
         return
     E, L, H, B = 64, 4096, 4, 4
     q, k, v, do = attention_setup(torch, nnop, dev, E, L, H, B)
