@@ -515,7 +515,8 @@ SWEEP = [  # (E, L, H, KH, B, causal): bf16 attention fwd+bwd shapes around the 
     (64, 16384, 4, 4, 1, True), (64, 4096, 4, 4, 4, False), (64, 4096, 16, 4, 4, True), (64, 4096, 16, 16, 4, True),
     (128, 1024, 16, 16, 4, True), (128, 4096, 4, 4, 4, True), (128, 4096, 32, 8, 1, True),
     (128, 8192, 8, 2, 2, True), (128, 4096, 4, 4, 4, False), (32, 4096, 8, 8, 4, True), (16, 4096, 8, 8, 4, True),
-    (256, 2048, 4, 4, 2, True),
+    (256, 2048, 4, 4, 2, True), (256, 4096, 8, 8, 1, True), (64, 4096, 32, 8, 1, True), (64, 4096, 8, 1, 4, True),
+    (128, 2048, 32, 8, 2, True), (128, 4096, 8, 1, 4, True), (128, 4096, 32, 8, 4, True),
 ]
 
 

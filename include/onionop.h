@@ -106,9 +106,10 @@ int onionop_flash_attn_fwd(void* stream, int dtype,
                            void* o, float* ms, float* ls);
 
 /* Bytes of workspace the backward entry points use for these sizes: the log-sum-exp and
- * rowsum(dO o) of every query row, and, for a 16-bit call with a pair bias on a grid of
- * fewer than 192 four-head workgroups, float32 partial dQ rows of a key-range split.  A
- * workspace of only 8 bytes per query row plus 256 also works; the dQ then runs unsplit. */
+ * rowsum(dO o) of every query row, and, for 16-bit calls on small grids (with a pair
+ * bias, or GQA without one), float32 partial rows of the range splits that spread a dQ's
+ * keys or a dK / dV's queries over several workgroups.  A workspace of only 8 bytes per
+ * query row plus 256 also works; the kernels then run unsplit (same results to rounding). */
 size_t onionop_flash_attn_bwd_workspace(int dtype, int64_t E, int64_t QL, int64_t KL,
                                         int64_t QH, int64_t KH, int64_t B);
 

@@ -167,8 +167,9 @@ static size_t bwd_ws_base(int64_t QL, int64_t QH, int64_t B) {
 }
 
 // Layout of the range splits' partial rows after lse2 / delta (offsets from the 256-byte
-// aligned start, each 256-byte aligned): the dQ key ranges' rows, then the dK / dV query
-// ranges' rows; bytes 0 where a shape takes no split.
+// aligned start, each 256-byte aligned): the dK / dV query ranges' rows, then the dQ key
+// ranges' rows (pair bias only, so last: a workspace that holds only the first part still
+// serves the GQA dK/dV split); bytes 0 where a shape takes no split.
 struct BwdSplitLayout {
     size_t dq_off, dq_bytes, kv_off, kv_bytes;
 };
@@ -180,10 +181,10 @@ static BwdSplitLayout bwd_split_layout(int dtype, int64_t E, int64_t QL, int64_t
     const size_t rows = (size_t)QL * (size_t)QH * (size_t)B, rows_k = (size_t)KL * (size_t)KH * (size_t)B;
     const int nq = onionop::dq_key_splits(dtype, E, QL, KL, QH, B);
     const int nk = onionop::kv_query_splits(dtype, E, QL, KL, QH, KH, B);
-    l.dq_off = align256(2 * rows * sizeof(float));
-    l.dq_bytes = nq > 1 ? (size_t)nq * rows * (size_t)E * sizeof(float) : 0;
-    l.kv_off = align256(l.dq_off + l.dq_bytes);
+    l.kv_off = align256(2 * rows * sizeof(float));
     l.kv_bytes = nk > 1 ? 2 * (size_t)nk * rows_k * (size_t)E * sizeof(float) : 0;
+    l.dq_off = align256(l.kv_off + l.kv_bytes);
+    l.dq_bytes = nq > 1 ? (size_t)nq * rows * (size_t)E * sizeof(float) : 0;
     return l;
 }
 
@@ -192,7 +193,7 @@ size_t onionop_flash_attn_bwd_workspace(int dtype, int64_t E, int64_t QL, int64_
     const size_t base = bwd_ws_base(QL, QH, B);
     const BwdSplitLayout l = bwd_split_layout(dtype, E, QL, KL, QH, KH, B);
     if (base == 0 || (l.dq_bytes == 0 && l.kv_bytes == 0)) return base;
-    return 256 + (l.kv_bytes > 0 ? l.kv_off + l.kv_bytes : l.dq_off + l.dq_bytes);
+    return 256 + (l.dq_bytes > 0 ? l.dq_off + l.dq_bytes : l.kv_off + l.kv_bytes);
 }
 
 // Shared body of the backward entry points; `stages` selects which kernels run.
@@ -251,15 +252,19 @@ static int attn_bwd_common(const char* what, int stages, void* stream, int dtype
         const size_t rows = (size_t)QL * (size_t)QH * (size_t)B;
         a.lse2 = reinterpret_cast<float*>(base);
         a.delta = a.lse2 + rows;
-        // The range splits of the pair-biased kernels, each where the workspace holds it.
-        if (pair != nullptr && rope_cos == nullptr) {
+        // The range splits (pair-biased dQ and dK/dV, GQA dK/dV), each where the workspace
+        // holds it; with the fused RoPE only the GQA dK/dV one (its kernel rotates dK before
+        // writing the partials).
+        {
             const BwdSplitLayout l = bwd_split_layout(dtype, E, QL, KL, QH, KH, B);
             const size_t lead = base - reinterpret_cast<uintptr_t>(workspace);
-            if ((stages & onionop::kBwdDq) && l.dq_bytes > 0 && lead + l.dq_off + l.dq_bytes <= workspace_bytes) {
+            if (pair != nullptr && rope_cos == nullptr && (stages & onionop::kBwdDq) && l.dq_bytes > 0 &&
+                lead + l.dq_off + l.dq_bytes <= workspace_bytes) {
                 a.dq_part = reinterpret_cast<float*>(base + l.dq_off);
                 a.dq_splits = onionop::dq_key_splits(dtype, E, QL, KL, QH, B);
             }
-            if ((stages & onionop::kBwdDkDv) && l.kv_bytes > 0 && lead + l.kv_off + l.kv_bytes <= workspace_bytes) {
+            if ((stages & onionop::kBwdDkDv) && (rope_cos == nullptr || QH > KH) && l.kv_bytes > 0 &&
+                lead + l.kv_off + l.kv_bytes <= workspace_bytes) {
                 a.kv_part = reinterpret_cast<float*>(base + l.kv_off);
                 a.kv_splits = onionop::kv_query_splits(dtype, E, QL, KL, QH, KH, B);
             }

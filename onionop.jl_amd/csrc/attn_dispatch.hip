@@ -51,11 +51,23 @@ int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t
 }
 
 int kv_query_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B) {
-    if ((dt != 1 && dt != 2) || E > 64 || QH != KH || KH % 4 != 0 || QL <= 0 || KL <= 0 || B <= 0) return 1;
-    const int64_t nwg4 = ((KL + 63) / 64) * (KH / 4) * B;
-    if (nwg4 >= 192) return 1;
-    const int64_t bq = E >= 64 ? 32 : 64;  // the bias kernel's query tile
-    return split_count(256 / nwg4, (QL + bq - 1) / bq);
+    if ((dt != 1 && dt != 2) || E > 64 || KH <= 0 || QH % KH != 0 || QL <= 0 || KL <= 0 || B <= 0) return 1;
+    if (QH == KH) {  // pair bias, four kv heads per workgroup
+        if (KH % 4 != 0) return 1;
+        const int64_t nwg4 = ((KL + 63) / 64) * (KH / 4) * B;
+        if (nwg4 >= 192) return 1;
+        const int64_t bq = E >= 64 ? 32 : 64;  // the bias kernel's query tile
+        return split_count(256 / nwg4, (QL + bq - 1) / bq);
+    }
+    // GQA without a bias: the one-wave dK/dV grid (8-wave workgroups of 128 keys at E = 64
+    // while they make 256, one per CU; else 4-wave workgroups of 64 keys, two per CU),
+    // split towards 1024 workgroups over the rep q heads' 64-query tiles when it fills
+    // the chip at most once.
+    const int64_t nwg = ((KL + 63) / 64) * KH * B, nwg4 = ((KL + 127) / 128) * KH * B;
+    const bool wide = E == 64 && nwg4 >= 256;
+    const int64_t g = wide ? nwg4 : nwg;
+    if (g > (wide ? 256 : 512)) return 1;
+    return split_count(1024 / g, (QH / KH) * ((QL + 63) / 64));
 }
 
 int device_cu_count() {

@@ -38,8 +38,8 @@ struct AttnArgs {
     // the workspace, dq_splits x (B, QH, QL, E).
     float* dq_part = nullptr;
     int dq_splits = 1;
-    // Query-range split of the four-head bias dK / dV (kv_splits > 1): float32 partial
-    // rows, 2 x kv_splits x (B, KH, KL, E) (dK partials, then dV).
+    // Query-range split of the dK / dV (kv_splits > 1; four-head bias or GQA): float32
+    // partial rows, 2 x kv_splits x (B, KH, KL, E) (dK partials, then dV).
     float* kv_part = nullptr;
     int kv_splits = 1;
 };
@@ -72,8 +72,10 @@ int device_cu_count();
 // shape only: four-head workgroups on a grid of fewer than 192 of them take enough ranges
 // to make about 256 workgroups, at most 8, each of at least two 32-key tiles.
 int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t B);
-// Query ranges the dK / dV of such a call spreads over (1: none), by the same rule: four
-// kv heads per workgroup (QH = KH), ranges of at least two query tiles.
+// Query ranges the dK / dV spreads over (1: none), a function of the shape only: with a
+// pair bias (QH = KH) by the same rule as the dQ (four kv heads per workgroup); without
+// one, for GQA (QH > KH) on grids of fewer than 1024 one-wave dK/dV workgroups, towards
+// 1024 of them over the rep q heads' query tiles.  Ranges hold at least two tiles.
 int kv_query_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B);
 
 // Longest row (elements) the row-wise kernels keep in registers for dtype dt.

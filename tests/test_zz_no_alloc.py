@@ -1,16 +1,19 @@
 """onionop_flash_attn_bwd_noalloc: the attention backward without a workspace argument,
-whose workspace is the library's own device array, against onionop_flash_attn_bwd with a
-caller-allocated workspace.  Both run the same kernels on the same inputs, so the
-gradients must be identical bit for bit.  Two calls in a row, the second on a smaller
-problem (the array keeps the first call's contents), then a request beyond the array's
-size, which must be refused before anything is enqueued.
+whose workspace is the library's own 16 MiB device array, against onionop_flash_attn_bwd
+with a caller-allocated workspace of the same 16 MiB.  Both then run the same kernels on
+the same inputs (a workspace decides which range splits the backward may use), so the
+gradients must be identical bit for bit; against the full workspace the query reports
+they agree to the element type's tolerance (splits change only the summation order).
+Two calls in a row, the second on a smaller problem (the array keeps the first call's
+contents), then a request beyond the array's size, which must be refused before anything
+is enqueued.
 """
 import numpy as np
 import pytest
 import torch
 
 import nnop
-from helpers import make
+from helpers import TOL, host, make, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -24,21 +27,30 @@ def backward_both_ways(dev, dt, B, QH, KH, L, E, causal, with_pair, seed):
     pair = make(rng, (B, L, L, QH), dt, dev)[0] if with_pair else None
     print(f"no-alloc backward: {dt} B={B} QH={QH} KH={KH} L={L} E={E} causal={causal} pair={with_pair}", flush=True)
     o, ms, ls = nnop._flash_attention(q, k, v, pair, causal=causal)
-    ref = nnop.grad_flash_attention(do, o, ms, ls, q, k, v, pair, causal=causal)
+    full = nnop.grad_flash_attention(do, o, ms, ls, q, k, v, pair, causal=causal)  # full workspace
     L_ = nnop.lib()
     from nnop._util import dtype_code, ptr, stream_of
 
+    dtc, sc = dtype_code(q, "test"), nnop.attention_scale(E, dt)
+    ws = torch.empty(16 << 20, dtype=torch.uint8, device=dev)  # the library array's size
+    ref = [torch.full_like(q, 5.0), torch.full_like(k, 5.0), torch.full_like(v, 5.0)]
+    ref.append(torch.full_like(pair, 5.0) if with_pair else None)
+    nnop._lib.check(L_.onionop_flash_attn_bwd(
+        stream_of(q), dtc, E, L, L, QH, KH, B, ptr(do), ptr(o), ptr(ms), ptr(ls), ptr(q), ptr(k), ptr(v), ptr(pair),
+        None, int(causal), sc, 1, ptr(ref[0]), ptr(ref[1]), ptr(ref[2]), ptr(ref[3]), ptr(ws), ws.numel()))
     dq, dk, dv = torch.full_like(q, 3.0), torch.full_like(k, 3.0), torch.full_like(v, 3.0)
     dpair = torch.full_like(pair, 3.0) if with_pair else None
     st = L_.onionop_flash_attn_bwd_noalloc(
-        stream_of(q), dtype_code(q, "test"), E, L, L, QH, KH, B, ptr(do), ptr(o), ptr(ms), ptr(ls), ptr(q), ptr(k),
-        ptr(v), ptr(pair), None, int(causal), nnop.attention_scale(E, dt), 1, ptr(dq), ptr(dk), ptr(dv), ptr(dpair))
+        stream_of(q), dtc, E, L, L, QH, KH, B, ptr(do), ptr(o), ptr(ms), ptr(ls), ptr(q), ptr(k),
+        ptr(v), ptr(pair), None, int(causal), sc, 1, ptr(dq), ptr(dk), ptr(dv), ptr(dpair))
     nnop._lib.check(st)
     torch.cuda.synchronize()
-    for name, a, b in (("dq", dq, ref[0]), ("dk", dk, ref[1]), ("dv", dv, ref[2])):
+    for name, a, b, c in (("dq", dq, ref[0], full[0]), ("dk", dk, ref[1], full[1]), ("dv", dv, ref[2], full[2])):
         assert torch.equal(a, b), name
+        assert rel_err(host(a), host(c)) <= TOL[dt], name
     if with_pair:
         assert torch.equal(dpair, ref[3]), "dpair"
+        assert rel_err(host(dpair), host(full[3])) <= TOL[dt], "dpair"
 
 
 def test_noalloc_backward_matches_workspace_backward(dev):
