@@ -51,7 +51,14 @@ int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t
 }
 
 int kv_query_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B) {
-    if ((dt != 1 && dt != 2) || E > 64 || KH <= 0 || QH % KH != 0 || QL <= 0 || KL <= 0 || B <= 0) return 1;
+    if ((dt != 1 && dt != 2) || KH <= 0 || QH % KH != 0 || QL <= 0 || KL <= 0 || B <= 0) return 1;
+    if (E >= 128) {  // GQA of 8 or more q heads per kv head on the two-wave kernel (64 keys
+                     // per workgroup, 32-query tiles); fewer take two query-range groups
+        if (QH / KH < 8) return 1;
+        const int64_t nws = ((KL + 63) / 64) * KH * B;
+        if (nws > 512) return 1;
+        return split_count(1024 / nws, (QH / KH) * ((QL + 31) / 32));
+    }
     if (QH == KH) {  // pair bias, four kv heads per workgroup
         if (KH % 4 != 0) return 1;
         const int64_t nwg4 = ((KL + 63) / 64) * (KH / 4) * B;

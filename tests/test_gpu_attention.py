@@ -89,6 +89,10 @@ CASES = [
     ("f16", 128, 255, 512, 2, 2, 2, False, False, False),
     ("bf16", 16, 255, 511, 2, 2, 3, False, True, False),
     ("bf16", 32, 768, 768, 8, 8, 2, False, True, False),
+    # MQA at E >= 128 on small grids: the two-wave dK/dV's iterations split over workgroups
+    ("bf16", 128, 300, 300, 8, 1, 2, True, False, True),
+    ("f16", 128, 200, 333, 8, 1, 1, False, False, False),
+    ("bf16", 256, 130, 130, 8, 1, 1, True, False, False),
     ("bf16", 64, 1024, 1024, 4, 4, 2, True, False, False),
     ("bf16", 64, 256, 256, 2, 2, 3, True, True, True),
     ("bf16", 128, 512, 512, 4, 1, 2, True, False, False),
