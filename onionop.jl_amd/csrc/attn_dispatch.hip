@@ -52,12 +52,13 @@ int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t
 
 int kv_query_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B) {
     if ((dt != 1 && dt != 2) || KH <= 0 || QH % KH != 0 || QL <= 0 || KL <= 0 || B <= 0) return 1;
-    if (E >= 128) {  // GQA of 8 or more q heads per kv head on the two-wave kernel (64 keys
-                     // per workgroup, 32-query tiles); fewer take two query-range groups
-        if (QH / KH < 8) return 1;
-        const int64_t nws = ((KL + 63) / 64) * KH * B;
-        if (nws > 512) return 1;
-        return split_count(1024 / nws, (QH / KH) * ((QL + 31) / 32));
+    if (E >= 128) {  // the two-wave kernel: 64 keys per workgroup, 32-query tiles
+        const int64_t nws = ((KL + 63) / 64) * KH * B, tiles = (QH / KH) * ((QL + 31) / 32);
+        // GQA of 8 or more q heads per kv head; fewer take two query-range groups
+        if (QH / KH >= 8) return nws > 512 ? 1 : split_count(1024 / nws, tiles);
+        // E = 256 (one workgroup per CU) on a grid that fills the chip at most once
+        if (E >= 256 && nws <= 256) return split_count(512 / nws, tiles);
+        return 1;
     }
     if (QH == KH) {  // pair bias, four kv heads per workgroup
         if (KH % 4 != 0) return 1;

@@ -75,7 +75,9 @@ int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t
 // Query ranges the dK / dV spreads over (1: none), a function of the shape only: with a
 // pair bias (QH = KH) by the same rule as the dQ (four kv heads per workgroup); without
 // one, for GQA (QH > KH) on grids of fewer than 1024 one-wave dK/dV workgroups, towards
-// 1024 of them over the rep q heads' query tiles.  Ranges hold at least two tiles.
+// 1024 of them over the rep q heads' query tiles; at E >= 128 (the two-wave kernel) for
+// 8 or more q heads per kv head, and at E = 256 on grids of at most 256 workgroups
+// (towards 512).  Ranges hold at least two tiles.
 int kv_query_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t KH, int64_t B);
 
 // Longest row (elements) the row-wise kernels keep in registers for dtype dt.
