@@ -252,13 +252,13 @@ static int attn_bwd_common(const char* what, int stages, void* stream, int dtype
         const size_t rows = (size_t)QL * (size_t)QH * (size_t)B;
         a.lse2 = reinterpret_cast<float*>(base);
         a.delta = a.lse2 + rows;
-        // The range splits (pair-biased dQ and dK/dV, GQA dK/dV), each where the workspace
-        // holds it; with the fused RoPE only the GQA dK/dV one (its kernel rotates dK before
-        // writing the partials).
+        // The range splits (pair-biased dQ and dK/dV, GQA dK/dV, E = 256 dQ and dK/dV), each
+        // where the workspace holds it; with the fused RoPE only the GQA dK/dV one (its
+        // kernel rotates dK before writing the partials).
         {
             const BwdSplitLayout l = bwd_split_layout(dtype, E, QL, KL, QH, KH, B);
             const size_t lead = base - reinterpret_cast<uintptr_t>(workspace);
-            if (pair != nullptr && rope_cos == nullptr && (stages & onionop::kBwdDq) && l.dq_bytes > 0 &&
+            if ((pair != nullptr || E >= 256) && rope_cos == nullptr && (stages & onionop::kBwdDq) && l.dq_bytes > 0 &&
                 lead + l.dq_off + l.dq_bytes <= workspace_bytes) {
                 a.dq_part = reinterpret_cast<float*>(base + l.dq_off);
                 a.dq_splits = onionop::dq_key_splits(dtype, E, QL, KL, QH, B);

@@ -43,7 +43,12 @@ static int split_count(int64_t want, int64_t tiles) {
 }
 
 int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t B) {
-    if ((dt != 1 && dt != 2) || E > 64 || QH % 4 != 0 || QL <= 0 || KL <= 0 || B <= 0) return 1;
+    if ((dt != 1 && dt != 2) || QL <= 0 || KL <= 0 || QH <= 0 || B <= 0) return 1;
+    if (E >= 256) {  // without a bias: one workgroup per CU, a grid that fills the chip at most once
+        const int64_t nwg = ((QL + 63) / 64) * QH * B;
+        return nwg > 256 ? 1 : split_count(512 / nwg, (KL + 31) / 32);
+    }
+    if (E > 64 || QH % 4 != 0) return 1;
     const int64_t nwg4 = ((QL + 63) / 64) * (QH / 4) * B;
     if (nwg4 >= 192) return 1;  // the unsplit four-head grid already fills the chip
     const int64_t tiles = (KL + 31) / 32;

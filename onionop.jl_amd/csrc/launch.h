@@ -68,9 +68,11 @@ bool launch_rope(hipStream_t s, int dt, int64_t E, int64_t L, int64_t QH, int64_
 
 // Compute units of the current device (cached per device; 0 if the query fails).
 int device_cu_count();
-// Key ranges the dQ of a 16-bit pair-biased call spreads over (1: none), a function of the
-// shape only: four-head workgroups on a grid of fewer than 192 of them take enough ranges
-// to make about 256 workgroups, at most 8, each of at least two 32-key tiles.
+// Key ranges the dQ of a 16-bit call spreads over (1: none), a function of the shape only:
+// with a pair bias, four-head workgroups on a grid of fewer than 192 of them take enough
+// ranges to make about 256 workgroups; at E = 256 without one (causal), a grid of at most
+// 256 workgroups takes enough to make about 512.  At most 8 ranges, each of at least two
+// 32-key tiles.
 int dq_key_splits(int dt, int64_t E, int64_t QL, int64_t KL, int64_t QH, int64_t B);
 // Query ranges the dK / dV spreads over (1: none), a function of the shape only: with a
 // pair bias (QH = KH) by the same rule as the dQ (four kv heads per workgroup); without

@@ -146,9 +146,12 @@ def test_fp32_qk_fp16_mode_no_bias(dev, causal):
 
 # E = 256 (the largest head dim the reference's group-size search admits on a 64 KiB-LDS
 # device, src/attention.jl:213-225): one wave per SIMD; float32 and the bias paths use
-# scratch for part of their registers.
+# scratch for part of their registers.  The 16-bit causal cases without a bias run the
+# backward's key- and query-range splits (small grids), with ranges of odd tile counts.
 @pytest.mark.parametrize("case", [
     ("bf16", 256, 130, 130, 2, 2, 1, True, False, False),
+    ("f16", 256, 200, 200, 2, 2, 1, True, False, True),
+    ("bf16", 256, 300, 300, 4, 2, 1, True, False, False),
     ("bf16", 256, 257, 200, 4, 2, 2, False, False, True),
     ("f16", 256, 100, 100, 2, 1, 1, True, True, False),
     ("f32", 256, 70, 70, 2, 2, 1, False, True, True),
