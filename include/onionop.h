@@ -107,7 +107,7 @@ int onionop_flash_attn_fwd(void* stream, int dtype,
 
 /* Bytes of workspace the backward entry points use for these sizes: the log-sum-exp and
  * rowsum(dO o) of every query row, and, for 16-bit calls on small grids (with a pair
- * bias, or GQA without one), float32 partial rows of the range splits that spread a dQ's
+ * bias, GQA, or E = 256), float32 partial rows of the range splits that spread a dQ's
  * keys or a dK / dV's queries over several workgroups.  A workspace of only 8 bytes per
  * query row plus 256 also works; the kernels then run unsplit (same results to rounding). */
 size_t onionop_flash_attn_bwd_workspace(int dtype, int64_t E, int64_t QL, int64_t KL,
