@@ -270,6 +270,8 @@ def test_errors_match_reference_messages(dev):
     ("bf16", 64, 300, 4, 2, True, False, False),
     ("f16", 128, 257, 2, 2, True, False, True),
     ("f32", 32, 200, 4, 4, False, True, True),
+    ("bf16", 256, 300, 4, 2, True, False, False),  # dQ key- and dK/dV query-range splits
+    ("bf16", 32, 256, 8, 8, False, True, False),   # the four-head bias kernels' splits
 ])
 def test_staged_backward_matches_combined(dev, dt, E, L, QH, KH, causal, use_pair, use_kpad):
     """The staged entry points (preprocess, dK/dV, dQ) and the combined backward (dQ with
