@@ -58,6 +58,12 @@ def test_noalloc_backward_matches_workspace_backward(dev):
     backward_both_ways(dev, torch.float16, 1, 4, 4, 300, 32, False, True, seed=2)
 
 
+def test_noalloc_backward_head_dim_256(dev):
+    """E = 256 on a small causal grid: the dQ key-range and dK/dV query-range partials
+    (about 9 MB) fit the array, so both entry points take the same splits."""
+    backward_both_ways(dev, torch.bfloat16, 1, 2, 2, 300, 256, True, False, seed=3)
+
+
 def test_noalloc_backward_refuses_oversized_requests(dev):
     L_ = nnop.lib()
     # 4 x 64 x 8192 query rows need 16 MiB + 256 bytes: more than the array holds
